@@ -1,0 +1,247 @@
+"""CPU checks that pin the oracle (oracle/attention.py) before it is trusted.
+
+The reference holds no golden vectors for this path, so each oracle function
+is pinned by (a) torch's SDPA MATH routine, (b) closed forms and invariants
+that a plausible mistake breaks (dropped max subtraction, wrong scale
+placement, transposed operand, missing rescale), (c) brute-force loops on tiny
+inputs and (d) the committed fixtures in tests/golden/. The last block plants
+mistakes in copies of the oracle and asserts the checks catch them.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attn_golden.npz")
+
+
+def rand(shape, seed, mult=1.0):
+    return np.random.default_rng(seed).standard_normal(shape) * mult
+
+
+def brute_force(q, k, v, scale):
+    """Per-element loops in Python floats (tiny inputs only)."""
+    Sq, D = q.shape
+    Skv = k.shape[0]
+    out = np.zeros((Sq, v.shape[1]))
+    for i in range(Sq):
+        s = [scale * sum(q[i, d] * k[j, d] for d in range(D)) for j in range(Skv)]
+        mx = max(s)
+        e = [np.exp(x - mx) for x in s]
+        tot = sum(e)
+        for d in range(v.shape[1]):
+            out[i, d] = sum(e[j] * v[j, d] for j in range(Skv)) / tot
+    return out
+
+
+# -- attention_fp64 -----------------------------------------------------------
+
+def test_fp64_matches_brute_force():
+    q, k, v = rand((5, 8), 1), rand((7, 8), 2), rand((7, 8), 3)
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, 0.3), brute_force(q, k, v, 0.3),
+                               rtol=0, atol=1e-13)
+
+
+def test_fp64_matches_torch_sdpa_math_fp64():
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    q, k, v = rand((2, 3, 37, 64), 4), rand((2, 3, 83, 64), 5), rand((2, 3, 83, 64), 6)
+    with sdpa_kernel(SDPBackend.MATH):
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), scale=0.125).numpy()
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, 0.125), ref, rtol=0, atol=1e-12)
+
+
+def test_single_key_is_v0():
+    q, k, v = rand((9, 16), 7), rand((1, 16), 8), rand((1, 16), 9)
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, 1.7), np.repeat(v, 9, 0), atol=0)
+
+
+def test_zero_query_is_mean_of_v():
+    q, k, v = np.zeros((4, 32)), rand((50, 32), 10), rand((50, 32), 11)
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, 0.5), np.tile(v.mean(0), (4, 1)),
+                               atol=1e-14)
+
+
+def test_one_hot_v_gives_probabilities():
+    q, k = rand((6, 16), 12), rand((10, 16), 13)
+    s = q @ k.T * 0.25
+    p = np.exp(s) / np.exp(s).sum(1, keepdims=True)   # no max shift needed at this size
+    np.testing.assert_allclose(oa.attention_fp64(q, k, np.eye(10), 0.25), p, atol=1e-14)
+
+
+def test_score_shift_invariance():
+    # Adding c*q_hat to every key adds the same constant to all scores of that row.
+    q, k, v = rand((1, 32), 14), rand((40, 32), 15), rand((40, 32), 16)
+    k2 = k + 3.0 * q / np.linalg.norm(q)
+    np.testing.assert_allclose(oa.attention_fp64(q, k2, v, 0.2), oa.attention_fp64(q, k, v, 0.2),
+                               atol=1e-12)
+
+
+def test_permutation_invariance_and_equivariance():
+    q, k, v = rand((12, 16), 17), rand((30, 16), 18), rand((30, 16), 19)
+    pk = np.random.default_rng(0).permutation(30)
+    pq = np.random.default_rng(1).permutation(12)
+    base = oa.attention_fp64(q, k, v, 0.3)
+    np.testing.assert_allclose(oa.attention_fp64(q, k[pk], v[pk], 0.3), base, atol=1e-13)
+    np.testing.assert_allclose(oa.attention_fp64(q[pq], k, v, 0.3), base[pq], atol=1e-13)
+
+
+def test_scale_folding():
+    q, k, v = rand((8, 16), 20), rand((25, 16), 21), rand((25, 16), 22)
+    np.testing.assert_allclose(oa.attention_fp64(4.0 * q, k, v, 0.1),
+                               oa.attention_fp64(q, k, v, 0.4), atol=1e-13)
+
+
+def test_large_margin_key_selects_its_value():
+    q = np.zeros((1, 8)); q[0, 0] = 1.0
+    k = np.zeros((5, 8)); k[3, 0] = 100.0
+    v = rand((5, 8), 23)
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, 1.0)[0], v[3], atol=1e-30)
+
+
+def test_convex_hull():
+    q, k, v = rand((20, 16), 24, 3.0), rand((33, 16), 25, 3.0), rand((33, 16), 26)
+    o = oa.attention_fp64(q, k, v, 0.5)
+    assert (o >= v.min(0) - 1e-12).all() and (o <= v.max(0) + 1e-12).all()
+
+
+def test_empty_keys_give_zeros():
+    assert not oa.attention_fp64(rand((3, 8), 27), np.zeros((0, 8)), np.zeros((0, 8)), 1.0).any()
+    assert not oa.online_softmax_tiled(rand((3, 8), 27), np.zeros((0, 8)), np.zeros((0, 8)),
+                                       1.0).any()
+
+
+# -- sdpa_math_fp32 / chunked ---------------------------------------------------
+
+def test_sdpa_math_fp32_matches_fp64():
+    q, k, v = oa.make_inputs(1, 2, 70, 130, 64, seed=28)
+    mx, mn = oa.error_stats(oa.sdpa_math_fp32(q, k, v, 0.125), oa.attention_fp64(q, k, v, 0.125))
+    assert mx < 5e-6 and mn < 1e-6
+
+
+def test_chunked_sdpa_equals_unchunked():
+    q, k, v = oa.make_inputs(2, 2, 300, 90, 32, seed=29)
+    a = oa.chunked_sdpa_math(q, k, v, 0.2, rows=64)
+    b = oa.sdpa_math_fp32(q, k, v, 0.2)
+    assert (a - b).abs().max().item() < 1e-6
+
+
+# -- online_softmax_tiled (reference state machine) ----------------------------
+
+@pytest.mark.parametrize("tile", [1, 7, 16, 64, 1000])
+def test_tiled_online_softmax_equals_direct(tile):
+    # model_check.py:139-153 checks its own restatement at 1e-5 on 37 x 83.
+    q, k, v = rand((1, 2, 37, 64), 30), rand((1, 2, 83, 64), 31), rand((1, 2, 83, 64), 32)
+    np.testing.assert_allclose(oa.online_softmax_tiled(q, k, v, 0.125, tile),
+                               oa.attention_fp64(q, k, v, 0.125), atol=1e-12)
+
+
+def test_tiled_online_softmax_rising_scores():
+    # Scores increasing along keys: every tile raises the running max.
+    q = np.ones((1, 4, 8))
+    k = np.linspace(0, 20, 50)[None, :, None] * np.ones((1, 50, 8))
+    v = rand((1, 50, 8), 33)
+    np.testing.assert_allclose(oa.online_softmax_tiled(q, k, v, 0.5, 4),
+                               oa.attention_fp64(q, k, v, 0.5), atol=1e-12)
+
+
+# -- kernel_numerics_model -------------------------------------------------------
+
+@pytest.mark.parametrize("name,rows", [("c1", 1024), ("c3", 64), ("c2", 32)])
+def test_kernel_numerics_model_meets_tolerance(name, rows):
+    """The gfx950 kernel's rounding design stays inside the north-star bar on
+    row slices of the BASELINE configs (c3 is the binding one, survey 8c)."""
+    B, H, Sq, Skv, D, qm, vm, seed = oa.CONFIGS[name]
+    q, k, v = oa.make_inputs(B, min(H, 2), min(Sq, rows), Skv, D, qm, vm, seed)
+    out = oa.kernel_numerics_model(q, k, v, D ** -0.5)
+    ok, mx, mn = oa.within_tolerance(out, oa.attention_fp64(q, k, v, D ** -0.5))
+    assert ok, (mx, mn)
+
+
+def test_kernel_numerics_model_negative_and_zero_scale():
+    q, k, v = oa.make_inputs(1, 1, 40, 90, 64, seed=34)
+    for s in (-0.125, 0.0):
+        ok, mx, mn = oa.within_tolerance(oa.kernel_numerics_model(q, k, v, s),
+                                         oa.attention_fp64(q, k, v, s))
+        assert ok, (s, mx, mn)
+
+
+# -- golden fixtures -----------------------------------------------------------------
+
+def golden_cases():
+    with np.load(GOLDEN) as z:
+        names = sorted({key.split("/")[0] for key in z.files})
+        return [(n, z[f"{n}/q"], z[f"{n}/k"], z[f"{n}/v"], float(z[f"{n}/scale"]), z[f"{n}/o"])
+                for n in names]
+
+
+def test_golden_fixture_count():
+    assert len(golden_cases()) == 12
+
+
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c[0])
+def test_oracle_reproduces_golden(case):
+    name, q, k, v, scale, o = case
+    assert q.dtype == np.float16
+    np.testing.assert_allclose(oa.attention_fp64(q, k, v, scale), o, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(oa.online_softmax_tiled(q, k, v, scale, 16), o, rtol=0, atol=1e-12)
+    ok, mx, mn = oa.within_tolerance(
+        oa.sdpa_math_fp32(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), scale), o)
+    assert ok, (mx, mn)
+
+
+# -- planted mistakes: the checks above must reject a wrong oracle ---------------
+
+def _no_max_shift(q, k, v, scale):
+    s = np.einsum("...id,...jd->...ij", q, k) * scale
+    p = np.exp(s)
+    return np.einsum("...ij,...jd->...id", p / p.sum(-1, keepdims=True), v)
+
+
+def _scale_outside_exp(q, k, v, scale):
+    s = np.einsum("...id,...jd->...ij", q, k)
+    p = np.exp(s - s.max(-1, keepdims=True)) * scale
+    return np.einsum("...ij,...jd->...id", p / p.sum(-1, keepdims=True), v)
+
+
+def _transposed_v(q, k, v, scale):
+    s = np.einsum("...id,...jd->...ij", q, k) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("...ij,...dj->...id", p, v[..., :v.shape[-1], :v.shape[-2]].swapaxes(-1, -2)
+                     .swapaxes(-1, -2))
+
+
+def _tiled_no_rescale(q, k, v, scale, tile_n=16):
+    Skv = k.shape[-2]
+    m = np.full(q.shape[:-1], -np.inf)
+    l = np.zeros(q.shape[:-1])
+    acc = np.zeros(q.shape[:-1] + (v.shape[-1],))
+    for n0 in range(0, Skv, tile_n):
+        s = np.einsum("...id,...jd->...ij", q, k[..., n0:n0 + tile_n, :]) * scale
+        m = np.maximum(m, s.max(-1))
+        e = np.exp(s - m[..., None])
+        acc = acc + np.einsum("...ij,...jd->...id", e, v[..., n0:n0 + tile_n, :])
+        l = l + e.sum(-1)
+    return acc / l[..., None]
+
+
+def test_planted_mistakes_are_caught():
+    q, k, v = rand((1, 1, 37, 64), 40, 1.5), rand((1, 1, 83, 64), 41, 1.5), rand((1, 1, 83, 64), 42)
+    ref = oa.attention_fp64(q, k, v, 0.125)
+    # Golden values differ from every mutant by far more than the bar.
+    for bad in (_scale_outside_exp, _tiled_no_rescale):
+        assert np.abs(bad(q, k, v, 0.125) - ref).max() > 1e-2, bad.__name__
+    # The max shift is invisible at small scores but overflows at large ones.
+    with np.errstate(over="ignore", invalid="ignore"):
+        big = _no_max_shift(q * 100, k, v, 1.0)
+    assert not np.isfinite(big).all()
+    # A mis-indexed V contraction fails the one-hot closed form.
+    qs, ks = rand((6, 10), 43), rand((10, 10), 44)
+    assert np.abs(_transposed_v(qs, ks, np.arange(100.0).reshape(10, 10), 0.25)
+                  - oa.attention_fp64(qs, ks, np.arange(100.0).reshape(10, 10), 0.25)).max() > 1
