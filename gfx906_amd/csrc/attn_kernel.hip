@@ -16,15 +16,21 @@
 //    online-softmax state (running max m, running sum l) is a per-lane scalar
 //    and the row reductions need a single exchange with lane^32.
 //  * The same registers, rounded to fp16, are the B operand of
-//    O^T = V^T * P^T. The key order inside each 16-key step of that MFMA
-//    follows the accumulator layout; V^T is stored in LDS with the matching
-//    key permutation (bits 2 and 3 of the key index swapped), so a lane's A
-//    operand is one 16-byte LDS read.
+//    O^T = V^T * P^T. V stays row-major ([key][dim]) in LDS and the A operand
+//    is read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane
+//    four keys of one dim; the key order is chosen to match the accumulator
+//    layout of S^T.
+//  * K and V tiles go from HBM straight into LDS with global_load_lds_dwordx4
+//    (no VGPR staging), through a two-stage ring: the loads of tile t+1 are in
+//    flight while tile t is computed, with one workgroup barrier per tile.
+//    Rows are XOR-swizzled in 16-byte units so that the QK^T reads
+//    (32 keys x one 16-byte unit) and the transposed V reads (8 keys x 64
+//    bytes) are free of LDS bank conflicts.
 //  * Softmax runs in fp32 with exp2 and scale*log2(e) folded into one FMA.
 //    The running max is updated lazily: the O accumulator is rescaled only
 //    when a tile's max exceeds the running max by more than 2^8, which keeps
-//    every p = exp2(s*c - m) <= 256 (exact in fp16 range) and skips the
-//    rescale multiply on almost every tile.
+//    every p = exp2(s*c - m) <= 256 and skips the rescale on almost every
+//    tile.
 //  * The row sum l is accumulated from the fp16-rounded P (v_dot2_f32_f16
 //    against 1.0), so numerator and denominator see the same rounded weights.
 //  * Output rows are normalised by 1/l and rounded to fp16 (RNE), as the
@@ -33,6 +39,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+#include <type_traits>
 
 #include "../../include/gfx906_amd_attn.h"
 
@@ -42,18 +49,25 @@ typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+#define LDS_AS __attribute__((address_space(3)))
+#define GLOBAL_AS __attribute__((address_space(1)))
 
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy-rescale threshold in log2 units: p never exceeds 2^kTau.
 constexpr float kTau = 8.0f;
 
-__device__ __forceinline__ f16x8 ld16(const f16* p) {
+__device__ __forceinline__ f16x8 ld_global16(const f16* p) {
     return *reinterpret_cast<const f16x8*>(p);
 }
-__device__ __forceinline__ void st16(f16* p, f16x8 v) {
-    *reinterpret_cast<f16x8*>(p) = v;
+
+// Three-way max; with NaN-free arithmetic assumed (-fno-honor-nans) the
+// backend selects v_max3_f32 for it.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    return fmaxf(fmaxf(a, b), c);
 }
 
 __device__ __forceinline__ float xor32_max(float x) {
@@ -63,119 +77,113 @@ __device__ __forceinline__ float xor32_sum(float x) {
     return x + __shfl_xor(x, 32);
 }
 
-// Position of key kk (0..15) inside a 16-key step of the V^T tile: bits 2 and
-// 3 swapped, so the 8 keys one lane feeds into the PV MFMA are contiguous.
-__device__ __forceinline__ constexpr int vt_pos(int kk) {
-    return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+// 16-byte LDS read at a byte address.
+__device__ __forceinline__ f16x8 lds_read16(const char* base, int byte_off) {
+    return *(const LDS_AS f16x8*)((const LDS_AS char*)base + byte_off);
+}
+// Transposed 8-byte LDS read (see the 16-lane mapping in the header comment).
+__device__ __forceinline__ f16x4 lds_read_tr(const char* base, int byte_off) {
+    fp16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (LDS_AS fp16x4_t*)((LDS_AS char*)base + byte_off));
+    return __builtin_bit_cast(f16x4, r);
 }
 
 // Kernel configuration per head-dim class.
 //   DP  : head dim the tiles are built for (64, 128 or 512)
 //   NW  : waves per workgroup; each wave owns 32 query rows
 //   BN  : keys per K/V tile
-template <int DP_, int NW_, int BN_>
+//   OCC : waves per SIMD the register budget is sized for
+template <int DP_, int NW_, int BN_, int OCC_>
 struct Cfg {
-    static constexpr int DP = DP_;
-    static constexpr int NW = NW_;
-    static constexpr int BN = BN_;
-    static constexpr int BM = NW * 32;           // query rows per workgroup
-    static constexpr int NT = NW * 64;           // threads per workgroup
-    static constexpr int KS = DP + 8;            // sK row stride (halfs)
-    static constexpr int VS = BN + 8;            // sVt row stride (halfs)
-    static constexpr int K_CHUNKS = BN * DP / 8; // 16-byte chunks per K tile
-    static constexpr int V_TASKS = (DP / 8) * (BN / 4); // 4 keys x 8 dims each
-    static constexpr int K_PER_T = (K_CHUNKS + NT - 1) / NT;
-    static constexpr int V_PER_T = (V_TASKS + NT - 1) / NT;
-    static constexpr int LDS_BYTES = (BN * KS + DP * VS) * 2;
+    static constexpr int DP = DP_, NW = NW_, BN = BN_, OCC = OCC_;
+    static constexpr int BM = NW * 32;          // query rows per workgroup
+    static constexpr int NT = NW * 64;          // threads per workgroup
+    static constexpr int NU = DP / 8;           // 16-byte units per row
+    static constexpr int RB = DP * 2;           // bytes per row
+    static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
+    static constexpr int STAGE = 2 * TILE;      // K tile then V tile
+    static constexpr int NSTAGE = 2;
+    static constexpr int LDS = NSTAGE * STAGE;
+    static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
+    static_assert(BLKS % NW == 0, "tile must split evenly over waves");
+    static_assert(BN % 32 == 0 && DP % 32 == 0, "tile shape");
 };
 
-// One K/V tile staged in registers between its global load and its LDS store.
-template <class C>
-struct Stage {
-    f16x8 k[C::K_PER_T];
-    f16x8 v[C::V_PER_T][4];
-};
+// XOR swizzles of the 16-byte unit index within a row.
+//  K: the QK^T read takes one unit from 32 consecutive rows, so 16
+//     consecutive rows must land on 16 different bank groups.
+//  V: the transposed read takes 4 units from 8 consecutive rows; each half
+//     wave (4 rows x 4 units) must cover all 16 bank groups.
+template <int NU>
+__device__ __forceinline__ int kswz(int r) { return NU >= 16 ? (r & 15) : ((r >> 1) & 7); }
+template <int NU>
+__device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 
-// Global -> registers for key tile starting at n0. Keys >= Skv and dims >= D
-// are loaded as zeros (zero K columns meet zero Q columns; zero V rows meet
-// p = 0), so nothing outside the tensors is read.
+// Per-lane byte offsets of the direct HBM->LDS tile loads. Each wave fills
+// whole 1 KB LDS blocks (lane i writes 16-byte unit i of its block) for
+// BLKS/NW blocks of the K tile and as many of the V tile. The offsets are
+// relative to the tile's first row and do not change from tile to tile.
+// Units past D (padded head dims) are pointed at unit 0 of the row: finite
+// data that meets zero Q columns (K) or feeds unused output columns (V).
 template <class C, bool PAD>
-__device__ __forceinline__ void load_tile(Stage<C>& st, const f16* __restrict__ Kh,
-                                          const f16* __restrict__ Vh, int n0, int Skv,
-                                          int D, int tid) {
-    constexpr int CPR = C::DP / 8;  // chunks per row
+__device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
+                                             int (&voff)[C::BLKS / C::NW], int D, int wave,
+                                             int lane) {
 #pragma unroll
-    for (int i = 0; i < C::K_PER_T; ++i) {
-        const int c = tid + i * C::NT;
-        const int key = c / CPR, dc = c % CPR;
-        f16x8 val = {};
-        if ((C::K_CHUNKS % C::NT == 0 || c < C::K_CHUNKS) && n0 + key < Skv &&
-            (!PAD || dc * 8 < D))
-            val = ld16(Kh + (long)(n0 + key) * D + dc * 8);
-        st.k[i] = val;
-    }
-#pragma unroll
-    for (int i = 0; i < C::V_PER_T; ++i) {
-        const int t = tid + i * C::NT;
-        const int dc = t % CPR, kq = t / CPR;  // 8-dim block, 4-key quad
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int key = kq * 4 + r;
-            f16x8 val = {};
-            if ((C::V_TASKS % C::NT == 0 || t < C::V_TASKS) && n0 + key < Skv &&
-                (!PAD || dc * 8 < D))
-                val = ld16(Vh + (long)(n0 + key) * D + dc * 8);
-            st.v[i][r] = val;
-        }
+    for (int i = 0; i < C::BLKS / C::NW; ++i) {
+        const int unit = (wave + i * C::NW) * 64 + lane;
+        const int row = unit / C::NU, slot = unit % C::NU;
+        int ck = slot ^ kswz<C::NU>(row), cv = slot ^ vswz<C::NU>(row);
+        if (PAD && ck * 8 >= D) ck = 0;
+        if (PAD && cv * 8 >= D) cv = 0;
+        koff[i] = (row * D + ck * 8) * 2;
+        voff[i] = (row * D + cv * 8) * 2;
     }
 }
 
-// Registers -> LDS. K keeps its [key][dim] layout; V is transposed to
-// [dim][key] with the vt_pos key permutation inside each 16-key step.
+// Issue the loads of the K and V tiles starting at key n0 into one LDS stage.
+// The buffer descriptors cover exactly the tile's valid rows, so rows past
+// Skv read as zeros and nothing outside the tensors is touched.
+#if defined(__HIP_DEVICE_COMPILE__)
 template <class C>
-__device__ __forceinline__ void store_tile(const Stage<C>& st, f16* sK, f16* sVt, int tid) {
-    constexpr int CPR = C::DP / 8;
+__device__ __forceinline__ void issue_tile(const f16* __restrict__ Kh, const f16* __restrict__ Vh,
+                                           int n0, int Skv, int D, char* stage, int wave,
+                                           const int (&koff)[C::BLKS / C::NW],
+                                           const int (&voff)[C::BLKS / C::NW]) {
+    const int bytes = min(Skv - n0, C::BN) * D * 2;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + (long)n0 * D), 0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + (long)n0 * D), 0, bytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < C::K_PER_T; ++i) {
-        const int c = tid + i * C::NT;
-        if (C::K_CHUNKS % C::NT == 0 || c < C::K_CHUNKS) {
-            const int key = c / CPR, dc = c % CPR;
-            st16(sK + key * C::KS + dc * 8, st.k[i]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < C::V_PER_T; ++i) {
-        const int t = tid + i * C::NT;
-        if (C::V_TASKS % C::NT == 0 || t < C::V_TASKS) {
-            const int dc = t % CPR, kq = t / CPR;
-            const int key0 = kq * 4;  // 4-aligned, so vt_pos keeps the quad contiguous
-            const int pos = (key0 & ~15) + vt_pos(key0 & 15);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                f16x4 col = {st.v[i][0][e], st.v[i][1][e], st.v[i][2][e], st.v[i][3][e]};
-                *reinterpret_cast<f16x4*>(sVt + (dc * 8 + e) * C::VS + pos) = col;
-            }
-        }
+    for (int i = 0; i < C::BLKS / C::NW; ++i) {
+        char* dk = stage + (wave + i * C::NW) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)dk, 16, koff[i], 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(dk + C::TILE), 16, voff[i], 0,
+                                                 0, 0);
     }
 }
+#endif
 
 // grid: ceil(Sq / BM) * B*H workgroups, query tiles of one head adjacent;
 // block: NW*64 threads.
 template <class C, bool PAD>
-__global__ void __launch_bounds__(C::NT)
+__global__ void __launch_bounds__(C::NT, C::OCC)
 attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
               const f16* __restrict__ V, f16* __restrict__ O,
               int Sq, int Skv, int D, float c, float qsign) {
-    constexpr int DP = C::DP, BN = C::BN;
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int DP = C::DP, BN = C::BN, NU = C::NU, RB = C::RB;
     constexpr int NQF = DP / 16;  // Q fragments (16 dims each)
     constexpr int NOB = DP / 32;  // 32-dim output blocks
     constexpr int NKB = BN / 32;  // 32-key score blocks per tile
-    __shared__ __attribute__((aligned(16))) f16 sK[BN * C::KS];
-    __shared__ __attribute__((aligned(16))) f16 sVt[DP * C::VS];
+    constexpr int NKS = BN / 16;  // 16-key PV steps per tile
+    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, r32 = lane & 31;
+    const int j16 = lane & 15, G = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
     const long bh = blockIdx.x / nqt;
     const int qt = blockIdx.x % nqt;
@@ -186,15 +194,37 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
     const int qrow = qt * C::BM + wave * 32 + r32;
     const bool live = qrow < Sq;
 
+    const int ntiles = (Skv + BN - 1) / BN;
+    int koff[C::BLKS / C::NW], voff[C::BLKS / C::NW];
+    tile_offsets<C, PAD>(koff, voff, D, wave, lane);
+    if (ntiles > 0) issue_tile<C>(Kh, Vh, 0, Skv, D, lds, wave, koff, voff);
+
     // Q^T fragments: B operand (column = this lane's query, k = dims).
     f16x8 qf[NQF];
 #pragma unroll
     for (int s = 0; s < NQF; ++s) {
         const int d0 = 16 * s + 8 * g;
         f16x8 val = {};
-        if (live && (!PAD || d0 < D)) val = ld16(Qh + (long)qrow * D + d0);
+        if (live && (!PAD || d0 < D)) val = ld_global16(Qh + (long)qrow * D + d0);
         if (qsign < 0.f) val = -val;  // exact: negative scale -> negated q, |scale|
         qf[s] = val;
+    }
+
+    // Per-lane LDS byte offsets (stage- and tile-relative parts are immediates).
+    int kaddr[8];
+    {
+        const int kl = g ^ kswz<NU>(r32);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kaddr[s] = r32 * RB + (((2 * s) & 15) ^ kl) * 16;
+    }
+    int vaddr[4];
+    {
+        const int vrow = 4 * g + (j16 >> 2);
+        const int vv = NU >= 16 ? (j16 >> 2) : (j16 >> 3);
+        const int w = 2 * (G & 1) + ((j16 & 3) >> 1);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            vaddr[b] = vrow * RB + (4 * (b ^ vv) + w) * 16 + 8 * (j16 & 1);
     }
 
     f32x16 oacc[NOB];
@@ -203,38 +233,52 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
     float m_run = -INFINITY;  // running max, in units of s*c (log2 domain)
     float l_run = 0.f;        // partial row sum over this lane's keys
 
-    const int ntiles = (Skv + BN - 1) / BN;
-    Stage<C> st;
-    if (ntiles > 0) load_tile<C, PAD>(st, Kh, Vh, 0, Skv, D, tid);
-
-    for (int t = 0; t < ntiles; ++t) {
+    auto tile = [&](int t, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
         const int n0 = t * BN;
-        __syncthreads();
-        store_tile<C>(st, sK, sVt, tid);
-        __syncthreads();
-        if (t + 1 < ntiles) load_tile<C, PAD>(st, Kh, Vh, n0 + BN, Skv, D, tid);
+        const char* sk = lds + (t & 1) * C::STAGE;
+        const char* sv = sk + C::TILE;
 
         // S^T = K Q^T over this tile.
         f32x16 sacc[NKB];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             sacc[kb] = f32x16{};
-            const f16* kp = sK + (kb * 32 + r32) * C::KS + 8 * g;
 #pragma unroll
-            for (int s = 0; s < NQF; ++s)
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld16(kp + 16 * s), qf[s],
-                                                                  sacc[kb], 0, 0, 0);
+            for (int s = 0; s < NQF; ++s) {
+                const f16x8 a = lds_read16(sk, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sacc[kb], 0, 0, 0);
+            }
+        }
+        // Keep a few K fragments in flight instead of all of them: 4 reads
+        // ahead, then one read per MFMA.
+        {
+            constexpr int N = NKB * NQF, AHEAD = N < 4 ? N : 4;
+            __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
+#pragma unroll
+            for (int i = 0; i < N - AHEAD; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
         }
 
-        // Tail tile: keys >= Skv take no part in the max and get p = 0.
-        const bool tail = n0 + BN > Skv;
-        float mx = -INFINITY;
+        if (MASK) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (key >= Skv) sacc[kb][r] = -INFINITY;
+                }
+        }
+        float mx = sacc[0][0];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = n0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (!tail || key < Skv) mx = fmaxf(mx, sacc[kb][r]);
+            for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2) {
+                if (r + 1 < 16) mx = max3(mx, sacc[kb][r], sacc[kb][r + 1]);
+                else mx = fmaxf(mx, sacc[kb][r]);
             }
         mx = xor32_max(mx) * c;
 
@@ -247,35 +291,51 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
             l_run *= alpha;
             m_run = m_new;
         }
+        const float nm = -m_run;
 
-        // P = exp2(S*c - m), rounded to fp16; l += sum of the rounded values.
+        // P = exp2(S*c - m) in fp16; l += sum of the rounded values; O^T += V^T P^T.
 #pragma unroll
-        for (int ks = 0; ks < BN / 16; ++ks) {
+        for (int ks = 0; ks < NKS; ++ks) {
             const int kb = ks >> 1, r0 = 8 * (ks & 1);
             f16x8 pb;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int r = r0 + e;
-                float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], c, -m_run));
-                if (tail) {
-                    const int key = n0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (key >= Skv) p = 0.f;
-                }
-                pb[e] = (f16)p;
-            }
-#pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                f16x2 pp = {pb[e], pb[e + 1]};
-                l_run = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+                float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + e], c, nm));
+                float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + e + 1], c, nm));
+                if (MASK) {
+                    const int key = n0 + kb * 32 + 8 * ((r0 + e) >> 2) + 4 * g + (e & 3);
+                    if (key >= Skv) p0 = 0.f;
+                    if (key + 1 >= Skv) p1 = 0.f;
+                }
+                const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+                pb[e] = h[0];
+                pb[e + 1] = h[1];
+                l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
             }
-            // O^T += V^T P^T for this 16-key step.
-            const f16* vp = sVt + r32 * C::VS + 16 * ks + 8 * g;
 #pragma unroll
-            for (int b = 0; b < NOB; ++b)
-                oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld16(vp + b * 32 * C::VS), pb,
-                                                                 oacc[b], 0, 0, 0);
+            for (int b = 0; b < NOB; ++b) {
+                const int off = ks * 16 * RB + (b & ~3) * 64;
+                const f16x4 lo = lds_read_tr(sv, vaddr[b & 3] + off);
+                const f16x4 hi = lds_read_tr(sv, vaddr[b & 3] + off + 8 * RB);
+                const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, oacc[b], 0, 0, 0);
+            }
         }
-    }
+    };
+
+    // Own loads of tile t complete, then every wave's: tile t is in LDS and
+    // all waves are done with tile t-1, whose stage the next loads reuse.
+    auto step = [&](int t, auto masked) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if (t + 1 < ntiles)
+            issue_tile<C>(Kh, Vh, (t + 1) * BN, Skv, D, lds + ((t + 1) & 1) * C::STAGE, wave, koff,
+                          voff);
+        tile(t, masked);
+    };
+    const int nfull = Skv / BN;  // tiles with no key past Skv
+    for (int t = 0; t < nfull; ++t) step(t, std::false_type{});
+    if (nfull < ntiles) step(nfull, std::true_type{});
 
     const float l = xor32_sum(l_run);
     const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -287,17 +347,21 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
             for (int rr = 0; rr < 4; ++rr) {
                 const int d0 = 32 * b + 8 * rr + 4 * g;
                 if (!PAD || d0 < D) {
-                    f16x4 h = {(f16)(oacc[b][4 * rr + 0] * inv), (f16)(oacc[b][4 * rr + 1] * inv),
-                               (f16)(oacc[b][4 * rr + 2] * inv), (f16)(oacc[b][4 * rr + 3] * inv)};
+                    const f16x2 h0 = __builtin_convertvector(
+                        f32x2{oacc[b][4 * rr + 0] * inv, oacc[b][4 * rr + 1] * inv}, f16x2);
+                    const f16x2 h1 = __builtin_convertvector(
+                        f32x2{oacc[b][4 * rr + 2] * inv, oacc[b][4 * rr + 3] * inv}, f16x2);
+                    const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
                     *reinterpret_cast<f16x4*>(op + d0) = h;
                 }
             }
     }
+#endif
 }
 
-using Cfg64 = Cfg<64, 4, 64>;
-using Cfg128 = Cfg<128, 4, 64>;
-using Cfg512 = Cfg<512, 4, 32>;
+using Cfg64 = Cfg<64, 4, 64, 2>;
+using Cfg128 = Cfg<128, 4, 64, 2>;
+using Cfg512 = Cfg<512, 4, 32, 1>;
 
 thread_local char g_err[256];
 
