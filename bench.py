@@ -1,0 +1,215 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 attention forward on its BASELINE.json metric.
+
+One step = one attention forward over the north-star workload
+(B=1, H=16, Sq=Skv=16384, D=128, fp16, scale 1/sqrt(D)), inputs already
+resident in HBM. Prints one JSON line with the driver's fields plus:
+
+* ``roofline``: the kernel's algorithmic TFLOP/s (4*B*H*Sq*Skv*D per launch,
+  flops_probe.py:18) from the average launch duration measured with HIP events
+  on the stream the kernel runs on, against MI355X's dense fp16 MFMA peak;
+  ``traffic`` is the HBM bytes per launch read from the committed rocprofv3
+  counter summary (profiles/), or null when that file is absent.
+* ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine) on
+  a bounded sample of the same workload: two heads, all query rows against
+  all keys, chunked by 2048 query rows.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attn fwd TFLOP/s + % fp16 MFMA peak, B1 H16 S16K D128, 1×MI355X"
+PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+WORKLOAD = dict(B=1, H=16, Sq=16384, Skv=16384, D=128)
+SEED = 106
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_pmc.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--workload", default="ns", choices=["ns", "c1", "c2", "c3", "c4", "c5"],
+                    help="BASELINE.json config to run (default: the north star the metric is "
+                         "quoted on; others are for profiling)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="instead of attention, time a plain device copy of this many bytes "
+                         "(reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    return ap.parse_args()
+
+
+def copy_calibration(nbytes, steps):
+    """Plain HBM copy of `nbytes` per launch: its FETCH_SIZE / WRITE_SIZE per
+    dispatch, divided by nbytes, is the scale factor for the counter runs."""
+    import torch
+
+    x = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    x.random_(0, 255)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        y.copy_(x)
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b) / steps
+    print(json.dumps({"copy_bytes": nbytes, "ms": round(ms, 4),
+                      "GB_per_s_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
+
+
+def read_profile_figures():
+    """HBM bytes per launch and counter ratios from the committed summary."""
+    out = {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None}
+    if not os.path.isfile(TRAFFIC_FILE):
+        return out
+    with open(TRAFFIC_FILE) as f:
+        text = f.read()
+    for key, name in (("traffic", "hbm_bytes_per_launch"), ("mfma_busy_pct", "mfma_busy_pct"),
+                      ("lds_bank_conflict_pct", "lds_bank_conflict_pct")):
+        m = re.search(rf"^{name}\s*[:=]\s*([0-9.eE+-]+)", text, re.M)
+        if m:
+            out[key] = float(m.group(1))
+    return out
+
+
+def cpu_baseline():
+    """torch SDPA MATH on CPU, fp32 upcast, 2 heads of the workload (min of 3)."""
+    import torch
+
+    from oracle.attention import make_inputs, time_cpu_sdpa
+
+    w = WORKLOAD
+    heads = 2
+    q, k, v = make_inputs(1, heads, w["Sq"], w["Skv"], w["D"], seed=SEED)
+    t = time_cpu_sdpa(q, k, v, w["D"] ** -0.5, reps=3)
+    flops = 4 * heads * w["Sq"] * w["Skv"] * w["D"]
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch SDPA MATH (fp32 upcast) on CPU, {heads} of {w['H']} heads, "
+                   f"Sq=Skv={w['Sq']}, D={w['D']}, chunked by 2048 query rows, min of 3 "
+                   f"after 1 warm-up: {t:.3f} s; os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the attention shards over heads with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    if args.copy_bytes:
+        copy_calibration(args.copy_bytes, args.steps)
+        return
+
+    import gfx906_amd
+    from oracle.attention import make_inputs
+
+    from oracle.attention import CONFIGS
+
+    if args.workload == "ns":
+        w, mults, seed = WORKLOAD, (1.0, 1.0), SEED
+    else:
+        B, H, Sq, Skv, D, qm, vm, seed = CONFIGS[args.workload]
+        w, mults = dict(B=B, H=H, Sq=Sq, Skv=Skv, D=D), (qm, vm)
+    q, k, v = (t.to("cuda") for t in make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"],
+                                                  *mults, seed=seed))
+    scale = w["D"] ** -0.5
+    attn = gfx906_amd.extension().attn
+    flops = gfx906_amd.flops(w["B"], w["H"], w["Sq"], w["Skv"], w["D"])
+
+    for _ in range(args.warmup):
+        attn(q, k, v, scale)
+    torch.cuda.synchronize()
+
+    # Per-launch HIP events on the stream the kernel runs on (the current stream).
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        attn(q, k, v, scale)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_ms = sum(kernel_ms) / len(kernel_ms)
+    ms_per_step = wall * 1e3 / args.steps
+    value = flops * args.steps / wall / 1e12
+    achieved = flops / (avg_ms * 1e-3) / 1e12
+
+    prof = read_profile_figures()
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: q,k,v ~ N(0,1) fp16 from a seeded CPU generator",
+        "config": {"workload": (f"attn_fwd B{w['B']} H{w['H']} Sq{w['Sq']} Skv{w['Skv']} "
+                                f"D{w['D']} fp16, scale 1/sqrt(D), no mask ("
+                                + ("BASELINE.json north star" if args.workload == "ns"
+                                   else f"BASELINE.json config {args.workload}") + ")"), **w,
+                   "parallelism": "single GPU"},
+        "pct_peak": round(100 * value / PEAK_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": prof["traffic"],
+            "kernel_ms_avg": round(avg_ms, 4),
+            "kernel_ms_min": round(min(kernel_ms), 4),
+            "algorithmic_flops_per_launch": flops,
+            "min_hbm_bytes_per_launch": 2 * (2 * w["B"] * w["H"] * w["Sq"] * w["D"]
+                                             + 2 * w["B"] * w["H"] * w["Skv"] * w["D"]),
+        },
+        "counters": {"mfma_busy_pct": prof["mfma_busy_pct"],
+                     "lds_bank_conflict_pct": prof["lds_bank_conflict_pct"],
+                     "source": os.path.relpath(TRAFFIC_FILE, ROOT)
+                     if os.path.isfile(TRAFFIC_FILE) else None},
+    }
+    if not args.no_cpu and args.workload == "ns":
+        result["cpu_baseline"] = cpu_baseline()
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

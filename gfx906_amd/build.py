@@ -55,7 +55,7 @@ def build_kernel_lib(extra_flags=()) -> Path:
     """Compile csrc/attn_kernel.hip into the C-ABI shared library."""
     LIB.mkdir(exist_ok=True)
     tmp = KERNEL_LIB.with_suffix(".so.tmp")
-    _run([hipcc(), *HIP_FLAGS, *extra_flags, "-shared",
+    _run([hipcc(), *HIP_FLAGS, *extra_flags, "-shared", f"-I{ROOT / 'include'}",
           str(CSRC / "attn_kernel.hip"), "-o", str(tmp)])
     os.replace(tmp, KERNEL_LIB)
     return KERNEL_LIB

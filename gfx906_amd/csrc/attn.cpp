@@ -14,7 +14,7 @@
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
 
-#include "../../include/gfx906_amd_attn.h"
+#include "gfx906_amd_attn.h"
 
 torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double scale) {
     TORCH_CHECK(q.is_cuda() && q.dtype() == torch::kHalf, "kernel: q must be a CUDA fp16 tensor");

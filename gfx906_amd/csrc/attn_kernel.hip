@@ -41,7 +41,7 @@
 #include <math.h>
 #include <type_traits>
 
-#include "../../include/gfx906_amd_attn.h"
+#include "gfx906_amd_attn.h"
 
 namespace {
 
@@ -52,6 +52,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_AS __attribute__((address_space(3)))
 #define GLOBAL_AS __attribute__((address_space(1)))
@@ -59,6 +60,9 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy-rescale threshold in log2 units: p never exceeds 2^kTau.
 constexpr float kTau = 8.0f;
+constexpr float kPmaxLimit = 256.0f;  // 2^kTau
+// sched_group_barrier instruction classes
+constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
 
 __device__ __forceinline__ f16x8 ld_global16(const f16* p) {
     return *reinterpret_cast<const f16x8*>(p);
@@ -68,13 +72,6 @@ __device__ __forceinline__ f16x8 ld_global16(const f16* p) {
 // backend selects v_max3_f32 for it.
 __device__ __forceinline__ float max3(float a, float b, float c) {
     return fmaxf(fmaxf(a, b), c);
-}
-
-__device__ __forceinline__ float xor32_max(float x) {
-    return fmaxf(x, __shfl_xor(x, 32));
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-    return x + __shfl_xor(x, 32);
 }
 
 // 16-byte LDS read at a byte address.
@@ -101,11 +98,13 @@ struct Cfg {
     static constexpr int NU = DP / 8;           // 16-byte units per row
     static constexpr int RB = DP * 2;           // bytes per row
     static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
-    static constexpr int STAGE = 2 * TILE;      // K tile then V tile
-    static constexpr int NSTAGE = 2;
-    static constexpr int LDS = NSTAGE * STAGE;
+    static constexpr int LDS = 4 * TILE;        // two stages of (K tile, V tile)
     static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
     static_assert(BLKS % NW == 0, "tile must split evenly over waves");
+    // D = 512 holds its O accumulator in a whole SIMD's register file: its
+    // loops are scheduled explicitly and its QK^T contraction is split.
+    static constexpr bool INTERLEAVE = DP >= 512;
+    static constexpr int NCH = DP >= 512 ? 2 : 1;
     static_assert(BN % 32 == 0 && DP % 32 == 0, "tile shape");
 };
 
@@ -121,7 +120,7 @@ __device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 *
 
 // Per-lane byte offsets of the direct HBM->LDS tile loads. Each wave fills
 // whole 1 KB LDS blocks (lane i writes 16-byte unit i of its block) for
-// BLKS/NW blocks of the K tile and as many of the V tile. The offsets are
+// BLKS/NW blocks of each K tile and as many of each V tile. The offsets are
 // relative to the tile's first row and do not change from tile to tile.
 // Units past D (padded head dims) are pointed at unit 0 of the row: finite
 // data that meets zero Q columns (K) or feeds unused output columns (V).
@@ -141,44 +140,61 @@ __device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
     }
 }
 
-// Issue the loads of the K and V tiles starting at key n0 into one LDS stage.
-// The buffer descriptors cover exactly the tile's valid rows, so rows past
-// Skv read as zeros and nothing outside the tensors is touched.
 #if defined(__HIP_DEVICE_COMPILE__)
+// Issue the loads of one K (or V) tile starting at key n0 into an LDS stage.
+// The buffer descriptor covers exactly the tile's valid rows, so rows past
+// Skv read as zeros and nothing outside the tensor is touched.
 template <class C>
-__device__ __forceinline__ void issue_tile(const f16* __restrict__ Kh, const f16* __restrict__ Vh,
-                                           int n0, int Skv, int D, char* stage, int wave,
-                                           const int (&koff)[C::BLKS / C::NW],
-                                           const int (&voff)[C::BLKS / C::NW]) {
+__device__ __forceinline__ void issue_tile(const f16* __restrict__ X, int n0, int Skv, int D,
+                                           char* stage, int wave,
+                                           const int (&off)[C::BLKS / C::NW]) {
     const int bytes = min(Skv - n0, C::BN) * D * 2;
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + (long)n0 * D), 0, bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + (long)n0 * D), 0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(X + (long)n0 * D), 0, bytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < C::BLKS / C::NW; ++i) {
-        char* dk = stage + (wave + i * C::NW) * 1024;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)dk, 16, koff[i], 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(dk + C::TILE), 16, voff[i], 0,
-                                                 0, 0);
-    }
+    for (int i = 0; i < C::BLKS / C::NW; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)(stage + (wave + i * C::NW) * 1024),
+                                                 16, off[i], 0, 0, 0);
+}
+
+// Max of x over lanes l and l^32 (both halves get the result).
+__device__ __forceinline__ float half_swap_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 #endif
 
 // grid: ceil(Sq / BM) * B*H workgroups, query tiles of one head adjacent;
 // block: NW*64 threads.
+//
+// Per key tile t (one workgroup barrier each):
+//  * the loads of tile t+1 are issued into the other LDS stage;
+//  * S^T = K_t Q^T is computed 32 keys at a time, and each 32-key block is
+//    turned into P = exp2(S c - m) with the running max m as soon as its
+//    MFMAs finish, so the VALU work overlaps the remaining QK^T MFMAs;
+//  * if any p exceeds 2^kTau (the tile max jumped above the running max by
+//    more than kTau, or this is the first tile), the exact tile max is taken,
+//    O is rescaled and P recomputed from the scores still in registers;
+//  * O^T += V_t^T P^T.
 template <class C, bool PAD>
 __global__ void __launch_bounds__(C::NT, C::OCC)
 attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
               const f16* __restrict__ V, f16* __restrict__ O,
               int Sq, int Skv, int D, float c, float qsign) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int DP = C::DP, BN = C::BN, NU = C::NU, RB = C::RB;
+    constexpr int DP = C::DP, BN = C::BN, NU = C::NU, RB = C::RB, TILE = C::TILE;
     constexpr int NQF = DP / 16;  // Q fragments (16 dims each)
     constexpr int NOB = DP / 32;  // 32-dim output blocks
     constexpr int NKB = BN / 32;  // 32-key score blocks per tile
     constexpr int NKS = BN / 16;  // 16-key PV steps per tile
-    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];
+    constexpr int NCH = C::NCH;   // partial QK^T accumulators per score block
+    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];  // 2 stages x (K, V)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -197,17 +213,24 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
     const int ntiles = (Skv + BN - 1) / BN;
     int koff[C::BLKS / C::NW], voff[C::BLKS / C::NW];
     tile_offsets<C, PAD>(koff, voff, D, wave, lane);
-    if (ntiles > 0) issue_tile<C>(Kh, Vh, 0, Skv, D, lds, wave, koff, voff);
+    auto stage = [&](int t) __attribute__((always_inline)) { return lds + (t & 1) * 2 * TILE; };
+    auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
+        issue_tile<C>(Kh, t * BN, Skv, D, dst, wave, koff);
+        issue_tile<C>(Vh, t * BN, Skv, D, dst + TILE, wave, voff);
+    };
+    if (ntiles > 0) issue(0, stage(0));
 
-    // Q^T fragments: B operand (column = this lane's query, k = dims).
+    // Q^T fragments: B operand (column = this lane's query, k = dims). A
+    // negative scale is applied as negated q with |scale|: flipping the fp16
+    // sign bits is exact.
     f16x8 qf[NQF];
+    const unsigned qneg = qsign < 0.f ? 0x80008000u : 0u;
 #pragma unroll
     for (int s = 0; s < NQF; ++s) {
         const int d0 = 16 * s + 8 * g;
         f16x8 val = {};
         if (live && (!PAD || d0 < D)) val = ld_global16(Qh + (long)qrow * D + d0);
-        if (qsign < 0.f) val = -val;  // exact: negative scale -> negated q, |scale|
-        qf[s] = val;
+        qf[s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
     }
 
     // Per-lane LDS byte offsets (stage- and tile-relative parts are immediates).
@@ -230,114 +253,147 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
     f32x16 oacc[NOB];
 #pragma unroll
     for (int b = 0; b < NOB; ++b) oacc[b] = f32x16{};
-    float m_run = -INFINITY;  // running max, in units of s*c (log2 domain)
-    float l_run = 0.f;        // partial row sum over this lane's keys
+    // Running max, in units of s*c (log2 domain). It starts finite so that a
+    // masked key (score -inf) gives p = 0 rather than NaN on the first tile.
+    float m_run = -1e30f;
+    float l_run = 0.f;  // partial row sum over this lane's keys
 
-    auto tile = [&](int t, auto masked) {
+    // P for one 32-key block (two 16-key PV steps) with running max -nm.
+    // Adds the block's row-sum contribution, taken from the fp16-rounded
+    // values, to lsum, and folds the block's P into the packed running max pm.
+    auto block_exp = [&](const f32x16& Sb, f16x8& P0, f16x8& P1, float nm, float& lsum,
+                         f16x2& pm) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f16x8& P = h ? P1 : P0;
+#pragma unroll
+            for (int e = 0; e < 8; e += 4) {
+                f16x2 hp[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 2 * u], c, nm));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 2 * u + 1], c, nm));
+                    hp[u] = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+                    P[e + 2 * u] = hp[u][0];
+                    P[e + 2 * u + 1] = hp[u][1];
+                    lsum = __builtin_amdgcn_fdot2(hp[u], f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+                }
+                pm = __builtin_elementwise_maximum(pm, __builtin_elementwise_maximum(hp[0], hp[1]));
+            }
+        }
+    };
+
+    // One key tile. The stage pointers are restrict-qualified: the stage being
+    // filled and the stage being read are disjoint, and saying so lets the
+    // compiler read the current stage without first waiting for the new loads.
+    auto tile = [&](int t, auto masked, char* __restrict__ nxt, const char* __restrict__ cur) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(masked)::value;
-        const int n0 = t * BN;
-        const char* sk = lds + (t & 1) * C::STAGE;
-        const char* sv = sk + C::TILE;
+        if (t + 1 < ntiles) issue(t + 1, nxt);
+        const char* sk = cur;
+        const char* sv = cur + TILE;
 
-        // S^T = K Q^T over this tile.
-        f32x16 sacc[NKB];
+        // S^T = K Q^T, 32 keys at a time; each block goes straight to P with
+        // the running max.
+        f32x16 S[NKB];
+        f16x8 P[NKS];
+        float l_tile = 0.f;
+        f16x2 pm = {(f16)0.0f, (f16)0.0f};
+        const float nm = -m_run;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            sacc[kb] = f32x16{};
+            // NCH independent partial sums over the head dim, so a long
+            // contraction (D = 512) is not one dependent MFMA chain.
+            f32x16 Sp[NCH];
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) Sp[ch] = f32x16{};
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
                 const f16x8 a = lds_read16(sk, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sacc[kb], 0, 0, 0);
+                Sp[s % NCH] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], Sp[s % NCH], 0, 0, 0);
             }
-        }
-        // Keep a few K fragments in flight instead of all of them: 4 reads
-        // ahead, then one read per MFMA.
-        {
-            constexpr int N = NKB * NQF, AHEAD = N < 4 ? N : 4;
-            __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
+            if constexpr (C::INTERLEAVE) {
+                // One K fragment read ahead per MFMA instead of all of them.
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
 #pragma unroll
-            for (int i = 0; i < N - AHEAD; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int i = 0; i < NQF - 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+            S[kb] = Sp[0];
+#pragma unroll
+            for (int ch = 1; ch < NCH; ++ch) S[kb] += Sp[ch];
+            if (MASK) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = t * BN + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (key >= Skv) S[kb][r] = -INFINITY;
+                }
+            }
+            block_exp(S[kb], P[2 * kb], P[2 * kb + 1], nm, l_tile, pm);
         }
 
-        if (MASK) {
+        // Some p > 2^kTau (or +inf) means the running max is too low for this
+        // tile: take the exact max of the scores, rescale O and l, and redo P.
+        // The branch is per wave, so it stays uniform.
+        const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+        if (__builtin_expect(__any(pmax > kPmaxLimit), 0)) {
+            float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = n0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (key >= Skv) sacc[kb][r] = -INFINITY;
-                }
-        }
-        float mx = sacc[0][0];
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2) {
-                if (r + 1 < 16) mx = max3(mx, sacc[kb][r], sacc[kb][r + 1]);
-                else mx = fmaxf(mx, sacc[kb][r]);
-            }
-        mx = xor32_max(mx) * c;
-
-        // Lazy rescale, decided per wave so the branch is uniform.
-        if (__any(mx > m_run + kTau)) {
+                for (int r = 0; r < 16; r += 2) mx = max3(mx, S[kb][r], S[kb][r + 1]);
+            mx = half_swap_max(mx) * c;
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
             for (int b = 0; b < NOB; ++b) oacc[b] *= alpha;
             l_run *= alpha;
             m_run = m_new;
+            l_tile = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+                block_exp(S[kb], P[2 * kb], P[2 * kb + 1], -m_run, l_tile, pm);
         }
-        const float nm = -m_run;
+        l_run += l_tile;
 
-        // P = exp2(S*c - m) in fp16; l += sum of the rounded values; O^T += V^T P^T.
+        // O^T += V^T P^T.
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            const int kb = ks >> 1, r0 = 8 * (ks & 1);
-            f16x8 pb;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + e], c, nm));
-                float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + e + 1], c, nm));
-                if (MASK) {
-                    const int key = n0 + kb * 32 + 8 * ((r0 + e) >> 2) + 4 * g + (e & 3);
-                    if (key >= Skv) p0 = 0.f;
-                    if (key + 1 >= Skv) p1 = 0.f;
-                }
-                const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-                pb[e] = h[0];
-                pb[e + 1] = h[1];
-                l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
-            }
+        for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
             for (int b = 0; b < NOB; ++b) {
                 const int off = ks * 16 * RB + (b & ~3) * 64;
                 const f16x4 lo = lds_read_tr(sv, vaddr[b & 3] + off);
                 const f16x4 hi = lds_read_tr(sv, vaddr[b & 3] + off + 8 * RB);
                 const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, oacc[b], 0, 0, 0);
+                oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[ks], oacc[b], 0, 0, 0);
             }
+        if constexpr (C::INTERLEAVE) {
+            // Two transposed reads ahead per MFMA instead of all of them.
+            constexpr int N = NKS * NOB;
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
+#pragma unroll
+            for (int i = 0; i < N - 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
         }
     };
 
     // Own loads of tile t complete, then every wave's: tile t is in LDS and
     // all waves are done with tile t-1, whose stage the next loads reuse.
-    auto step = [&](int t, auto masked) {
+    auto step = [&](int t, auto masked) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-        if (t + 1 < ntiles)
-            issue_tile<C>(Kh, Vh, (t + 1) * BN, Skv, D, lds + ((t + 1) & 1) * C::STAGE, wave, koff,
-                          voff);
-        tile(t, masked);
+        tile(t, masked, stage(t + 1), stage(t));
     };
     const int nfull = Skv / BN;  // tiles with no key past Skv
     for (int t = 0; t < nfull; ++t) step(t, std::false_type{});
     if (nfull < ntiles) step(nfull, std::true_type{});
 
-    const float l = xor32_sum(l_run);
+    const float l = half_swap_sum(l_run);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (live) {
         f16* op = Oh + (long)qrow * D;
@@ -359,9 +415,20 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
 #endif
 }
 
-using Cfg64 = Cfg<64, 4, 64, 2>;
-using Cfg128 = Cfg<128, 4, 64, 2>;
-using Cfg512 = Cfg<512, 4, 32, 1>;
+// Tile configurations per head-dim class (waves per workgroup, keys per
+// tile, waves per SIMD); the macros exist for tuning sweeps.
+#ifndef ATTN_CFG64
+#define ATTN_CFG64 8, 64, 2
+#endif
+#ifndef ATTN_CFG128
+#define ATTN_CFG128 8, 128, 2
+#endif
+#ifndef ATTN_CFG512
+#define ATTN_CFG512 4, 32, 1
+#endif
+using Cfg64 = Cfg<64, ATTN_CFG64>;
+using Cfg128 = Cfg<128, ATTN_CFG128>;
+using Cfg512 = Cfg<512, ATTN_CFG512>;
 
 thread_local char g_err[256];
 
@@ -375,7 +442,10 @@ template <class C, bool PAD>
 hipError_t launch_cfg(const void* q, const void* k, const void* v, void* o, int B, int H,
                       int Sq, int Skv, int D, float scale, hipStream_t s) {
     dim3 grid((unsigned)((Sq + C::BM - 1) / C::BM) * (unsigned)(B * H));
-    const float c = fabsf(scale) * kLog2e;
+    // Masked keys carry score -inf and rely on c > 0 (-inf * 0 is NaN). For
+    // scale == 0, c = 1e-30 gives exp2(s*c - m) == 1.0f exactly for every
+    // finite score, i.e. the same uniform weights as c == 0.
+    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
     const float qsign = scale < 0.f ? -1.f : 1.f;
     hipLaunchKernelGGL((attn_fwd_mfma<C, PAD>), grid, dim3(C::NT), 0, s,
                        (const f16*)q, (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, D, c,

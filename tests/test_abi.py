@@ -1,0 +1,99 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports
+every function include/gfx906_amd_attn.h declares, rejects bad arguments
+before touching the GPU, and the torch binding loads and validates inputs.
+No kernel is launched here."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+import gfx906_amd
+from gfx906_amd import loader
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gfx906_amd_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_reference_entry_point():
+    names = declared_functions()
+    assert "launch" in names and "attn_fwd" in names and "attn_last_error" in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(loader.KERNEL_LIB))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(loader.KERNEL_LIB)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(declared_functions()) <= exported
+
+
+def test_launch_signature_matches_reference():
+    # attn.cpp:4-5: void launch(const void*, const void*, const void*, void*,
+    #                           int,int,int,int,int, float, hipStream_t)
+    text = re.sub(r"\s+", " ", open(HEADER).read())
+    assert ("void launch(const void* q, const void* k, const void* v, void* o, int B, int H, "
+            "int Sq, int Skv, int D, float scale, hipStream_t stream);") in text
+
+
+@pytest.mark.parametrize("D", [0, 7, 72, 96, 100, 256, 1024])
+def test_bad_head_dim_rejected_without_launch(D):
+    lib = gfx906_amd.capi()
+    assert lib.attn_fwd(None, None, None, None, 1, 1, 4, 4, D, 0.1, None) == 1
+    assert b"head_dim" in lib.attn_last_error()
+    lib.launch(None, None, None, None, 1, 1, 4, 4, D, 0.1, None)
+    assert b"head_dim" in lib.attn_last_error()
+
+
+def test_negative_sizes_and_null_pointers_rejected():
+    lib = gfx906_amd.capi()
+    assert lib.attn_fwd(None, None, None, None, -1, 1, 4, 4, 64, 0.1, None) == 1
+    assert b"negative" in lib.attn_last_error()
+    assert lib.attn_fwd(None, None, None, None, 1, 1, 4, 4, 64, 0.1, None) == 1
+    assert b"null" in lib.attn_last_error()
+
+
+def test_empty_problem_is_a_no_op():
+    lib = gfx906_amd.capi()
+    assert lib.attn_fwd(None, None, None, None, 0, 4, 4, 4, 64, 0.1, None) == 0
+    assert lib.attn_last_error() is None
+
+
+def test_torch_extension_loads_and_validates_on_cpu():
+    ext = gfx906_amd.extension()
+    q = torch.zeros(1, 1, 4, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA fp16"):
+        ext.attn(q, q, q, 0.1)
+
+
+def test_load_attention_returns_none_without_gfx950():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    loader._attempted = False
+    assert gfx906_amd.load_attention() is None
+    assert not gfx906_amd.is_gfx950()
+
+
+def test_product_package_never_imports_oracle():
+    pkg = os.path.join(ROOT, "gfx906_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in re.sub(r"#.*|//.*", "", text), f
+
+
+def test_flops_formula():
+    # flops_probe.py:18: 4*B*H*S*S*D
+    assert gfx906_amd.flops(1, 16, 16384, 16384, 128) == 2_199_023_255_552
