@@ -52,6 +52,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_AS __attribute__((address_space(3)))
@@ -415,6 +416,266 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// D = 512: 16x16x32 MFMA tiles, 16 query rows per wave.
+//
+// With 32 query rows a wave would need a 256-register O accumulator; with 16
+// rows O^T is 32 blocks of 16x16 (128 registers) and two waves fit per SIMD.
+// Lane l = 16*g + i holds query i of the wave: the S^T = K Q^T accumulator of
+// a 16-key block gives it keys 4g..4g+3, so row reductions combine the four
+// lanes i, i+16, i+32, i+48. A 32-key tile is two score blocks feeding one
+// 16x16x32 PV step, whose B operand takes keys 4g..4g+3 of block 0 and of
+// block 1; V^T is read with ds_read_b64_tr_b16 in that key order.
+struct Cfg512 {
+    static constexpr int DP = 512, NW = 8, BN = 32, BM = NW * 16, NT = NW * 64;
+    static constexpr int RB = DP * 2;  // bytes of one K or V row in HBM
+    // LDS rows are padded instead of swizzled (one direct-load instruction
+    // fills exactly one row, so the padding costs nothing): with a 1040-byte
+    // K stride the QK^T read (16 rows, one 16-byte unit each) and with a
+    // 1056-byte V stride the transposed read (8 rows x 32 bytes per half
+    // wave) touch every bank group once.
+    static constexpr int KS = RB + 16, VS = RB + 32;
+    static constexpr int KTILE = BN * KS, VTILE = BN * VS, STAGE = KTILE + VTILE;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int NLD = BN / NW;  // rows loaded per wave per tile, per tensor
+};
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Sum / max over lanes i, i+16, i+32, i+48.
+__device__ __forceinline__ float quad_group_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float quad_group_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+#endif
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Rare path of the D = 512 kernel: the tile's scores exceed the running max by
+// more than kTau. Returns the new max, the rescale factor for O and l, and P
+// and the tile's row sum recomputed with the new max. Kept out of line (and
+// away from O, which stays in registers) so the hot loop does not reserve
+// registers for it.
+struct Rescale512 {
+    f16x8 P;
+    float m, alpha, l_tile;
+};
+__device__ __attribute__((noinline)) Rescale512 d512_rescale(f32x4 S0, f32x4 S1, float m_run,
+                                                             float c) {
+    float mx = fmaxf(max3(S0[0], S0[1], S0[2]), max3(S0[3], S1[0], S1[1]));
+    mx = quad_group_max(max3(mx, S1[2], S1[3])) * c;
+    Rescale512 r;
+    r.m = fmaxf(m_run, mx);
+    r.alpha = __builtin_amdgcn_exp2f(m_run - r.m);
+    const float nm = -r.m;
+    float lsum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const f32x4& Sb = u < 2 ? S0 : S1;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1)], c, nm));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1) + 1], c, nm));
+        const f16x2 hp = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+        r.P[2 * u] = hp[0];
+        r.P[2 * u + 1] = hp[1];
+        lsum = __builtin_amdgcn_fdot2(hp, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+    }
+    r.l_tile = lsum;
+    return r;
+}
+#endif
+
+// grid: ceil(Sq / 128) * B*H workgroups; block: 512 threads.
+__global__ void __launch_bounds__(Cfg512::NT, 1)
+attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
+              const f16* __restrict__ V, f16* __restrict__ O,
+              int Sq, int Skv, float c, float qsign) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using C = Cfg512;
+    constexpr int D = C::DP, BN = C::BN, RB = C::RB, NLD = C::NLD;
+    static_assert(NLD * C::NW == BN && D * 2 == 64 * 16, "one row per load instruction");
+    constexpr int NQF = D / 32;  // Q fragments (32 dims each)
+    constexpr int NOB = D / 16;  // 16-dim output blocks
+    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];  // 2 stages x (K, V)
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const int nqt = (Sq + C::BM - 1) / C::BM;
+    const long bh = blockIdx.x / nqt;
+    const int qt = blockIdx.x % nqt;
+    const f16* Qh = Q + bh * (long)Sq * D;
+    const f16* Kh = K + bh * (long)Skv * D;
+    const f16* Vh = V + bh * (long)Skv * D;
+    f16* Oh = O + bh * (long)Sq * D;
+    const int qrow = qt * C::BM + wave * 16 + i;
+    const bool live = qrow < Sq;
+
+    auto stage = [&](int t) { return lds + (t & 1) * C::STAGE; };
+    // Direct loads: one instruction per K or V row; lane l fetches dims
+    // 8l..8l+7. Rows past Skv read as zeros (the descriptor covers the valid
+    // rows only).
+    auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
+        const int bytes = min(Skv - t * BN, BN) * RB;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + (long)t * BN * D), 0, bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + (long)t * BN * D), 0, bytes, 0x00020000);
+#pragma unroll
+        for (int n = 0; n < NLD; ++n) {
+            const int row = wave + n * C::NW;  // wave-uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + row * C::KS), 16,
+                                                     lane * 16, row * RB, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(dst + C::KTILE + row * C::VS),
+                                                     16, lane * 16, row * RB, 0, 0);
+        }
+    };
+    const int ntiles = (Skv + BN - 1) / BN;
+    if (ntiles > 0) issue(0, stage(0));
+
+    // Q^T fragments (B operand: column = this lane's query, k = dims 32s+8g..).
+    f16x8 qf[NQF];
+    const unsigned qneg = qsign < 0.f ? 0x80008000u : 0u;
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+        f16x8 val = {};
+        if (live) val = ld_global16(Qh + (long)qrow * D + 32 * s + 8 * g);
+        qf[s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
+    }
+
+    // K read: row kb*16 + i, dims 32s + 8g.. ; V^T read (transposed, per
+    // 16-lane group g): row 4g + i/4 (+16 for the second key half), dims
+    // 16*db + 4*(i%4)..
+    const int kbase = i * C::KS + g * 16;
+    const int vbase = (4 * g + (i >> 2)) * C::VS + 8 * (i & 3);
+
+    f32x4 oacc[NOB];
+#pragma unroll
+    for (int b = 0; b < NOB; ++b) oacc[b] = f32x4{};
+    float m_run = -1e30f;  // running max (log2 units); finite, see attn_fwd_mfma
+    float l_run = 0.f;
+
+    // P (B operand of the PV step) from the two score blocks, with running max -nm.
+    auto make_p = [&](const f32x4 (&S)[2], f16x8& P, float nm, float& lsum, f16x2& pm)
+        __attribute__((always_inline)) {
+        f16x2 hp[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const f32x4& Sb = S[u >> 1];
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1)], c, nm));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1) + 1], c, nm));
+            hp[u] = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+            P[2 * u] = hp[u][0];
+            P[2 * u + 1] = hp[u][1];
+            lsum = __builtin_amdgcn_fdot2(hp[u], f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+        }
+        pm = __builtin_elementwise_maximum(pm, __builtin_elementwise_maximum(
+                                                   __builtin_elementwise_maximum(hp[0], hp[1]),
+                                                   __builtin_elementwise_maximum(hp[2], hp[3])));
+    };
+
+    auto tile = [&](int t, char* __restrict__ nxt, const char* __restrict__ cur)
+        __attribute__((always_inline)) {
+        if (t + 1 < ntiles) issue(t + 1, nxt);
+        const char* sk = cur;
+        const char* sv = cur + C::KTILE;
+        f32x4 S[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 Sp[2] = {f32x4{}, f32x4{}};
+#pragma unroll
+            for (int s = 0; s < NQF; ++s) {
+                const f16x8 a = lds_read16(sk, kbase + kb * 16 * C::KS + s * 64);
+                Sp[s & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s], Sp[s & 1], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
+#pragma unroll
+            for (int n = 0; n < NQF - 4; ++n) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
+            S[kb] = Sp[0] + Sp[1];
+        }
+        if (t * BN + BN > Skv) {  // last, partial tile
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t * BN + kb * 16 + 4 * g + r >= Skv) S[kb][r] = -INFINITY;
+        }
+        if (t == 0) {  // first tile: start from its exact max (O is still zero)
+            float mx = fmaxf(max3(S[0][0], S[0][1], S[0][2]), max3(S[0][3], S[1][0], S[1][1]));
+            m_run = quad_group_max(max3(mx, S[1][2], S[1][3])) * c;
+        }
+        f16x8 P;
+        float l_tile = 0.f;
+        f16x2 pm = {(f16)0.0f, (f16)0.0f};
+        make_p(S, P, -m_run, l_tile, pm);
+        const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+        // The O rescale runs on every tile (alpha = 1.0 exactly unless the rare
+        // path ran): a conditional in-place rescale of the 128-register
+        // accumulator costs more registers than two waves per SIMD allow, while
+        // 128 multiplies per tile hide under its 64 MFMAs.
+        float alpha = 1.f;
+        if (__builtin_expect(__any(pmax > kPmaxLimit), 0)) {
+            const Rescale512 r = d512_rescale(S[0], S[1], m_run, c);
+            alpha = r.alpha;
+            l_run *= r.alpha;
+            m_run = r.m;
+            P = r.P;
+            l_tile = r.l_tile;
+        }
+#pragma unroll
+        for (int b = 0; b < NOB; ++b) oacc[b] *= alpha;
+        l_run += l_tile;
+        // O^T += V^T P^T, one 16x16x32 MFMA per 16-dim block.
+#pragma unroll
+        for (int b = 0; b < NOB; ++b) {
+            const f16x4 lo = lds_read_tr(sv, vbase + 32 * b);
+            const f16x4 hi = lds_read_tr(sv, vbase + 32 * b + 16 * C::VS);
+            const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            oacc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P, oacc[b], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
+#pragma unroll
+        for (int n = 0; n < NOB - 2; ++n) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+    };
+
+    for (int t = 0; t < ntiles; ++t) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile t landed (this wave's part)
+        __syncthreads();                    // ... every wave's; stage t+1 free
+        tile(t, stage(t + 1), stage(t));
+    }
+
+    const float l = quad_group_sum(l_run);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (live) {
+        f16* op = Oh + (long)qrow * D + 4 * g;
+#pragma unroll
+        for (int b = 0; b < NOB; ++b) {
+            const f16x2 h0 = __builtin_convertvector(f32x2{oacc[b][0] * inv, oacc[b][1] * inv}, f16x2);
+            const f16x2 h1 = __builtin_convertvector(f32x2{oacc[b][2] * inv, oacc[b][3] * inv}, f16x2);
+            const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
+            *reinterpret_cast<f16x4*>(op + 16 * b) = h;
+        }
+    }
+#endif
+}
+
 // Tile configurations per head-dim class (waves per workgroup, keys per
 // tile, waves per SIMD); the macros exist for tuning sweeps.
 #ifndef ATTN_CFG64
@@ -423,12 +684,8 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
 #ifndef ATTN_CFG128
 #define ATTN_CFG128 8, 128, 2
 #endif
-#ifndef ATTN_CFG512
-#define ATTN_CFG512 4, 32, 1
-#endif
 using Cfg64 = Cfg<64, ATTN_CFG64>;
 using Cfg128 = Cfg<128, ATTN_CFG128>;
-using Cfg512 = Cfg<512, ATTN_CFG512>;
 
 thread_local char g_err[256];
 
@@ -450,6 +707,16 @@ hipError_t launch_cfg(const void* q, const void* k, const void* v, void* o, int 
     hipLaunchKernelGGL((attn_fwd_mfma<C, PAD>), grid, dim3(C::NT), 0, s,
                        (const f16*)q, (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, D, c,
                        qsign);
+    return hipGetLastError();
+}
+
+hipError_t launch_d512(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
+                       int Skv, float scale, hipStream_t s) {
+    dim3 grid((unsigned)((Sq + Cfg512::BM - 1) / Cfg512::BM) * (unsigned)(B * H));
+    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);  // see launch_cfg
+    const float qsign = scale < 0.f ? -1.f : 1.f;
+    hipLaunchKernelGGL(attn_fwd_d512, grid, dim3(Cfg512::NT), 0, s, (const f16*)q,
+                       (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, c, qsign);
     return hipGetLastError();
 }
 
@@ -483,7 +750,7 @@ extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, in
     else if (D == 64)
         e = launch_cfg<Cfg64, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
     else if (D == 512)
-        e = launch_cfg<Cfg512, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+        e = launch_d512(q, k, v, o, B, H, Sq, Skv, scale, s);
     else
         e = launch_cfg<Cfg64, true>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
     if (e != hipSuccess) {
