@@ -20,17 +20,19 @@
 //    is read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane
 //    four keys of one dim; the key order is chosen to match the accumulator
 //    layout of S^T.
-//  * K and V tiles go from HBM straight into LDS with global_load_lds_dwordx4
-//    (no VGPR staging), through a two-stage ring: the loads of tile t+1 are in
-//    flight while tile t is computed, with one workgroup barrier per tile.
-//    Rows are XOR-swizzled in 16-byte units so that the QK^T reads
-//    (32 keys x one 16-byte unit) and the transposed V reads (8 keys x 64
-//    bytes) are free of LDS bank conflicts.
+//  * K and V tiles go from HBM straight into LDS with buffer loads to LDS
+//    (no VGPR staging), through a ring of four stages, two tiles ahead of
+//    the compute. Rows are XOR-swizzled in 16-byte units so that the QK^T
+//    reads (32 keys x one 16-byte unit) and the transposed V reads (8 keys x
+//    64 bytes) are free of LDS bank conflicts.
+//  * Each wave is software-pipelined over 32-key blocks: the iteration for
+//    block j issues the PV MFMAs of block j-1 and the QK^T MFMAs of block
+//    j+1 while the VALU turns the scores of block j into P.
 //  * Softmax runs in fp32 with exp2 and scale*log2(e) folded into one FMA.
-//    The running max is updated lazily: the O accumulator is rescaled only
-//    when a tile's max exceeds the running max by more than 2^8, which keeps
-//    every p = exp2(s*c - m) <= 256 and skips the rescale on almost every
-//    tile.
+//    The running max is updated lazily: O is rescaled only when a block's
+//    row sum of p = exp2(s*c - m) exceeds 2^15 (the block's max rose well
+//    above the running max, or this is the first block), which keeps every p
+//    finite in fp16 and skips the rescale on almost every block.
 //  * The row sum l is accumulated from the fp16-rounded P (v_dot2_f32_f16
 //    against 1.0), so numerator and denominator see the same rounded weights.
 //  * Output rows are normalised by 1/l and rounded to fp16 (RNE), as the
@@ -59,7 +61,9 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 #define GLOBAL_AS __attribute__((address_space(1)))
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Lazy-rescale threshold in log2 units: p never exceeds 2^kTau.
+// Lazy rescale: a block whose lane row sum exceeds this takes the exact max.
+constexpr float kLsumLimit = 32768.0f;
+// Lazy-rescale threshold of the D = 512 kernel in log2 units: p <= 2^kTau.
 constexpr float kTau = 8.0f;
 constexpr float kPmaxLimit = 256.0f;  // 2^kTau
 // sched_group_barrier instruction classes
@@ -86,29 +90,6 @@ __device__ __forceinline__ f16x4 lds_read_tr(const char* base, int byte_off) {
     return __builtin_bit_cast(f16x4, r);
 }
 
-// Kernel configuration per head-dim class.
-//   DP  : head dim the tiles are built for (64, 128 or 512)
-//   NW  : waves per workgroup; each wave owns 32 query rows
-//   BN  : keys per K/V tile
-//   OCC : waves per SIMD the register budget is sized for
-template <int DP_, int NW_, int BN_, int OCC_>
-struct Cfg {
-    static constexpr int DP = DP_, NW = NW_, BN = BN_, OCC = OCC_;
-    static constexpr int BM = NW * 32;          // query rows per workgroup
-    static constexpr int NT = NW * 64;          // threads per workgroup
-    static constexpr int NU = DP / 8;           // 16-byte units per row
-    static constexpr int RB = DP * 2;           // bytes per row
-    static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
-    static constexpr int LDS = 4 * TILE;        // two stages of (K tile, V tile)
-    static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
-    static_assert(BLKS % NW == 0, "tile must split evenly over waves");
-    // D = 512 holds its O accumulator in a whole SIMD's register file: its
-    // loops are scheduled explicitly and its QK^T contraction is split.
-    static constexpr bool INTERLEAVE = DP >= 512;
-    static constexpr int NCH = DP >= 512 ? 2 : 1;
-    static_assert(BN % 32 == 0 && DP % 32 == 0, "tile shape");
-};
-
 // XOR swizzles of the 16-byte unit index within a row.
 //  K: the QK^T read takes one unit from 32 consecutive rows, so 16
 //     consecutive rows must land on 16 different bank groups.
@@ -133,10 +114,11 @@ __device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
     for (int i = 0; i < C::BLKS / C::NW; ++i) {
         const int unit = (wave + i * C::NW) * 64 + lane;
         const int row = unit / C::NU, slot = unit % C::NU;
-        int ck = slot ^ kswz<C::NU>(row), cv = slot ^ vswz<C::NU>(row);
+        int ck = slot ^ kswz<C::NU>(row);
         if (PAD && ck * 8 >= D) ck = 0;
-        if (PAD && cv * 8 >= D) cv = 0;
         koff[i] = (row * D + ck * 8) * 2;
+        int cv = slot ^ vswz<C::NU>(row);
+        if (PAD && cv * 8 >= D) cv = 0;
         voff[i] = (row * D + cv * 8) * 2;
     }
 }
@@ -144,12 +126,15 @@ __device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
 #if defined(__HIP_DEVICE_COMPILE__)
 // Issue the loads of one K (or V) tile starting at key n0 into an LDS stage.
 // The buffer descriptor covers exactly the tile's valid rows, so rows past
-// Skv read as zeros and nothing outside the tensor is touched.
+// Skv read as zeros and nothing outside the tensor is touched; a tile that
+// starts at or past Skv has an empty range and fills the stage with zeros.
 template <class C>
 __device__ __forceinline__ void issue_tile(const f16* __restrict__ X, int n0, int Skv, int D,
                                            char* stage, int wave,
                                            const int (&off)[C::BLKS / C::NW]) {
-    const int bytes = min(Skv - n0, C::BN) * D * 2;
+    // Uniform; readfirstlane keeps the descriptor in SGPRs (a clamp selected
+    // as a VALU op would otherwise force a waterfall loop around each load).
+    const int bytes = __builtin_amdgcn_readfirstlane(max(0, min(Skv - n0, C::BN)) * D * 2);
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc((void*)(X + (long)n0 * D), 0, bytes, 0x00020000);
 #pragma unroll
@@ -169,33 +154,90 @@ __device__ __forceinline__ float half_swap_sum(float x) {
                                                     false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+
+// P for one 32-key block of S^T (a lane's 16 scores, two 16-key PV steps):
+// p = exp2(s*c + nm) rounded to fp16, nm = -(running max). Adds the block's
+// row-sum contribution, taken from the fp16-rounded values, to lsum.
+__device__ __forceinline__ void block_exp_f16(const f32x16& Sb, f16x8& P0, f16x8& P1, float nm,
+                                              float c, float& lsum) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        f16x8& P = h ? P1 : P0;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e], c, nm));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 1], c, nm));
+            const f16x2 hp = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+            P[e] = hp[0];
+            P[e + 1] = hp[1];
+            lsum = __builtin_amdgcn_fdot2(hp, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+        }
+    }
+}
+
+// Whether a block's P needs the exact-max rescale: some lane's row sum over
+// the block exceeds 2^15 or is not finite. Every p <= lsum, so passing the
+// test keeps all p finite in fp16; the first block (running max -1e30,
+// p = inf) always fails it.
+__device__ __forceinline__ bool needs_rescale(float lsum) {
+    return __any(!(lsum <= kLsumLimit));
+}
 #endif
+
+// ---------------------------------------------------------------------------
+// D <= 128: software-pipelined waves, 32 * QB query rows each.
+//
+// The iteration for 32-key block j issues the PV MFMAs of block j-1 and the
+// QK^T MFMAs of block j+1 while the VALU turns the scores of block j into P,
+// so every stretch of a wave's instruction stream carries matrix and vector
+// work (two blocks of S and of P are live). With QB = 2 each K or V fragment
+// read from LDS feeds two MFMAs, at twice the accumulator registers.
+//
+// K/V tiles are 64 keys (two blocks) in a ring of four LDS stages, separate
+// arrays so that the compiler can tell their accesses apart (a read of one
+// stage then never waits for loads into another). The barrier that opens
+// tile w+1 follows the iteration that finished every read of tile w-1, whose
+// stage then takes tile w+3: loads run two tiles ahead. Tiles past the end
+// are loaded anyway, as zeros (empty buffer range), which keeps every wait
+// count static.
+//
+//   DP  : head dim the tiles are built for (64 or 128; D < 64 is padded)
+//   NW  : waves per workgroup
+//   QB  : 32-row query blocks per wave
+//   OCC : workgroups per CU the register budget is sized for
+template <int DP_, int NW_, int QB_, int OCC_>
+struct Cfg {
+    static constexpr int DP = DP_, NW = NW_, QB = QB_, OCC = OCC_, BN = 64;
+    static constexpr int BM = NW * 32 * QB;     // query rows per workgroup
+    static constexpr int NT = NW * 64;          // threads per workgroup
+    static constexpr int NU = DP / 8;           // 16-byte units per row
+    static constexpr int RB = DP * 2;           // bytes per row
+    static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
+    static constexpr int STAGE = 2 * TILE;      // K tile, then V tile
+    static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
+    static_assert(BLKS % NW == 0, "tile must split evenly over waves");
+    static_assert(DP % 32 == 0 && DP <= 128, "head-dim class");
+};
 
 // grid: ceil(Sq / BM) * B*H workgroups, query tiles of one head adjacent;
 // block: NW*64 threads.
-//
-// Per key tile t (one workgroup barrier each):
-//  * the loads of tile t+1 are issued into the other LDS stage;
-//  * S^T = K_t Q^T is computed 32 keys at a time, and each 32-key block is
-//    turned into P = exp2(S c - m) with the running max m as soon as its
-//    MFMAs finish, so the VALU work overlaps the remaining QK^T MFMAs;
-//  * if any p exceeds 2^kTau (the tile max jumped above the running max by
-//    more than kTau, or this is the first tile), the exact tile max is taken,
-//    O is rescaled and P recomputed from the scores still in registers;
-//  * O^T += V_t^T P^T.
+
 template <class C, bool PAD>
 __global__ void __launch_bounds__(C::NT, C::OCC)
-attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
-              const f16* __restrict__ V, f16* __restrict__ O,
-              int Sq, int Skv, int D, float c, float qsign) {
+attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
+             const f16* __restrict__ V, f16* __restrict__ O,
+             int Sq, int Skv, int D, float c, float qsign) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int DP = C::DP, BN = C::BN, NU = C::NU, RB = C::RB, TILE = C::TILE;
-    constexpr int NQF = DP / 16;  // Q fragments (16 dims each)
+    constexpr int DP = C::DP, NU = C::NU, RB = C::RB, TILE = C::TILE, QB = C::QB;
+    constexpr int NQF = DP / 16;  // Q fragments (16 dims each) per query block
     constexpr int NOB = DP / 32;  // 32-dim output blocks
-    constexpr int NKB = BN / 32;  // 32-key score blocks per tile
-    constexpr int NKS = BN / 16;  // 16-key PV steps per tile
-    constexpr int NCH = C::NCH;   // partial QK^T accumulators per score block
-    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];  // 2 stages x (K, V)
+    constexpr int LPT = C::BLKS / C::NW;  // loads per wave per K (or V) tile
+    static_assert(2 * LPT < 16, "vmcnt immediate");
+    constexpr int kWaitNext = 0x0F70 | (2 * LPT);  // vmcnt(one tile of loads)
+    __shared__ __attribute__((aligned(1024))) char st0[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) char st3[C::STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -208,210 +250,212 @@ attn_fwd_mfma(const f16* __restrict__ Q, const f16* __restrict__ K,
     const f16* Kh = K + bh * (long)Skv * D;
     const f16* Vh = V + bh * (long)Skv * D;
     f16* Oh = O + bh * (long)Sq * D;
-    const int qrow = qt * C::BM + wave * 32 + r32;
-    const bool live = qrow < Sq;
+    const int qrow0 = qt * C::BM + wave * 32 * QB + r32;  // this lane's rows: qrow0 + 32 qb
+    const int ntiles = (Skv + C::BN - 1) / C::BN;
 
-    const int ntiles = (Skv + BN - 1) / BN;
-    int koff[C::BLKS / C::NW], voff[C::BLKS / C::NW];
-    tile_offsets<C, PAD>(koff, voff, D, wave, lane);
-    auto stage = [&](int t) __attribute__((always_inline)) { return lds + (t & 1) * 2 * TILE; };
-    auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
-        issue_tile<C>(Kh, t * BN, Skv, D, dst, wave, koff);
-        issue_tile<C>(Vh, t * BN, Skv, D, dst + TILE, wave, voff);
-    };
-    if (ntiles > 0) issue(0, stage(0));
-
-    // Q^T fragments: B operand (column = this lane's query, k = dims). A
-    // negative scale is applied as negated q with |scale|: flipping the fp16
-    // sign bits is exact.
-    f16x8 qf[NQF];
+    // Q^T fragments (B operands), loaded before any tile so that the tile
+    // waits below also cover them. Negative scale: sign bits flipped.
+    f16x8 qf[QB][NQF];
     const unsigned qneg = qsign < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int s = 0; s < NQF; ++s) {
-        const int d0 = 16 * s + 8 * g;
-        f16x8 val = {};
-        if (live && (!PAD || d0 < D)) val = ld_global16(Qh + (long)qrow * D + d0);
-        qf[s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
-    }
-
-    // Per-lane LDS byte offsets (stage- and tile-relative parts are immediates).
-    int kaddr[8];
-    {
-        const int kl = g ^ kswz<NU>(r32);
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) kaddr[s] = r32 * RB + (((2 * s) & 15) ^ kl) * 16;
-    }
-    int vaddr[4];
-    {
-        const int vrow = 4 * g + (j16 >> 2);
-        const int vv = NU >= 16 ? (j16 >> 2) : (j16 >> 3);
-        const int w = 2 * (G & 1) + ((j16 & 3) >> 1);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            vaddr[b] = vrow * RB + (4 * (b ^ vv) + w) * 16 + 8 * (j16 & 1);
-    }
-
-    f32x16 oacc[NOB];
-#pragma unroll
-    for (int b = 0; b < NOB; ++b) oacc[b] = f32x16{};
-    // Running max, in units of s*c (log2 domain). It starts finite so that a
-    // masked key (score -inf) gives p = 0 rather than NaN on the first tile.
-    float m_run = -1e30f;
-    float l_run = 0.f;  // partial row sum over this lane's keys
-
-    // P for one 32-key block (two 16-key PV steps) with running max -nm.
-    // Adds the block's row-sum contribution, taken from the fp16-rounded
-    // values, to lsum, and folds the block's P into the packed running max pm.
-    auto block_exp = [&](const f32x16& Sb, f16x8& P0, f16x8& P1, float nm, float& lsum,
-                         f16x2& pm) __attribute__((always_inline)) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            f16x8& P = h ? P1 : P0;
-#pragma unroll
-            for (int e = 0; e < 8; e += 4) {
-                f16x2 hp[2];
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 2 * u], c, nm));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 2 * u + 1], c, nm));
-                    hp[u] = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-                    P[e + 2 * u] = hp[u][0];
-                    P[e + 2 * u + 1] = hp[u][1];
-                    lsum = __builtin_amdgcn_fdot2(hp[u], f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
-                }
-                pm = __builtin_elementwise_maximum(pm, __builtin_elementwise_maximum(hp[0], hp[1]));
-            }
+        for (int s = 0; s < NQF; ++s) {
+            const int d0 = 16 * s + 8 * g, row = qrow0 + 32 * qb;
+            f16x8 val = {};
+            if (row < Sq && (!PAD || d0 < D)) val = ld_global16(Qh + (long)row * D + d0);
+            qf[qb][s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
         }
-    };
 
-    // One key tile. The stage pointers are restrict-qualified: the stage being
-    // filled and the stage being read are disjoint, and saying so lets the
-    // compiler read the current stage without first waiting for the new loads.
-    auto tile = [&](int t, auto masked, char* __restrict__ nxt, const char* __restrict__ cur) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(masked)::value;
-        if (t + 1 < ntiles) issue(t + 1, nxt);
-        const char* sk = cur;
-        const char* sv = cur + TILE;
+    f32x16 oacc[QB][NOB];
+    float m_run[QB], l_run[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+        for (int b = 0; b < NOB; ++b) oacc[qb][b] = f32x16{};
+        // Running max in units of s*c (log2 domain). It starts finite so that
+        // a masked key (score -inf) gives p = 0 rather than NaN.
+        m_run[qb] = -1e30f;
+        l_run[qb] = 0.f;
+    }
 
-        // S^T = K Q^T, 32 keys at a time; each block goes straight to P with
-        // the running max.
-        f32x16 S[NKB];
-        f16x8 P[NKS];
-        float l_tile = 0.f;
-        f16x2 pm = {(f16)0.0f, (f16)0.0f};
-        const float nm = -m_run;
+    if (ntiles > 0) {
+        int koff[LPT], voff[LPT];
+        tile_offsets<C, PAD>(koff, voff, D, wave, lane);
+        auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
+            issue_tile<C>(Kh, t * C::BN, Skv, D, dst, wave, koff);
+            issue_tile<C>(Vh, t * C::BN, Skv, D, dst + TILE, wave, voff);
+        };
+        int kaddr[8];
+        {
+            const int kl = g ^ kswz<NU>(r32);
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-            // NCH independent partial sums over the head dim, so a long
-            // contraction (D = 512) is not one dependent MFMA chain.
-            f32x16 Sp[NCH];
+            for (int s = 0; s < 8; ++s) kaddr[s] = r32 * RB + (((2 * s) & 15) ^ kl) * 16;
+        }
+        int vaddr[4];
+        {
+            const int vrow = 4 * g + (j16 >> 2);
+            const int vv = NU >= 16 ? (j16 >> 2) : (j16 >> 3);
+            const int w = 2 * (G & 1) + ((j16 & 3) >> 1);
 #pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) Sp[ch] = f32x16{};
+            for (int b = 0; b < 4; ++b)
+                vaddr[b] = vrow * RB + (4 * (b ^ vv) + w) * 16 + 8 * (j16 & 1);
+        }
+
+        // S^T of 32-key block kb of the tile in stage st, both query blocks.
+        auto qk = [&](const char* st, int kb, f32x16 (&S)[QB]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) S[qb] = f32x16{};
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
-                const f16x8 a = lds_read16(sk, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
-                Sp[s % NCH] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], Sp[s % NCH], 0, 0, 0);
-            }
-            if constexpr (C::INTERLEAVE) {
-                // One K fragment read ahead per MFMA instead of all of them.
-                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
+                const f16x8 a = lds_read16(st, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
 #pragma unroll
-                for (int i = 0; i < NQF - 4; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+                for (int qb = 0; qb < QB; ++qb)
+                    S[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][s], S[qb], 0, 0, 0);
+            }
+        };
+        // O^T += V^T P^T for 32-key block kb of the tile in stage st.
+        auto pv = [&](const char* st, int kb, const f16x8 (&P)[QB][2]) __attribute__((always_inline)) {
+            const char* sv = st + TILE;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int b = 0; b < NOB; ++b) {
+                    const int off = (2 * kb + ks) * 16 * RB + (b & ~3) * 64;
+                    const f16x4 lo = lds_read_tr(sv, vaddr[b & 3] + off);
+                    const f16x4 hi = lds_read_tr(sv, vaddr[b & 3] + off + 8 * RB);
+                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        oacc[qb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[qb][ks], oacc[qb][b], 0, 0, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
+        };
+        // Scores of keys >= Skv (block keys key0..key0+31) to -inf. Taken
+        // for the last one or two blocks only; a branch at the start of an
+        // iteration, so the iteration's MFMAs and VALU work stay in one
+        // scheduling region.
+        auto mask = [&](f32x16 (&S)[QB], int key0) __attribute__((always_inline)) {
+            if (key0 + 32 > Skv) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        if (key >= Skv) S[qb][r] = -INFINITY;
+                    }
             }
-            S[kb] = Sp[0];
+        };
+        // P of one 32-key block for every query block, with the lazy rescale:
+        // when a row sum fails the test, the exact max of the block's scores
+        // is taken, O and l are rescaled and P is recomputed (a per-wave
+        // branch, so it stays uniform). Any rescale of O comes after the PV
+        // MFMAs issued before this call.
+        auto softmax = [&](f32x16 (&S)[QB], f16x8 (&P)[QB][2]) __attribute__((always_inline)) {
+            float lp[QB];
 #pragma unroll
-            for (int ch = 1; ch < NCH; ++ch) S[kb] += Sp[ch];
-            if (MASK) {
+            for (int qb = 0; qb < QB; ++qb) {
+                lp[qb] = 0.f;
+                block_exp_f16(S[qb], P[qb][0], P[qb][1], -m_run[qb], c, lp[qb]);
+            }
+            float lmax = lp[0];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = t * BN + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (key >= Skv) S[kb][r] = -INFINITY;
+            for (int qb = 1; qb < QB; ++qb) lmax = fmaxf(lmax, lp[qb]);
+            if (__builtin_expect(needs_rescale(lmax), 0)) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) mx = max3(mx, S[qb][r], S[qb][r + 1]);
+                    mx = half_swap_max(mx) * c;
+                    const float m_new = fmaxf(m_run[qb], mx);
+                    const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+#pragma unroll
+                    for (int b = 0; b < NOB; ++b) oacc[qb][b] *= alpha;
+                    l_run[qb] *= alpha;
+                    m_run[qb] = m_new;
+                    lp[qb] = 0.f;
+                    block_exp_f16(S[qb], P[qb][0], P[qb][1], -m_new, c, lp[qb]);
                 }
             }
-            block_exp(S[kb], P[2 * kb], P[2 * kb + 1], nm, l_tile, pm);
-        }
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) l_run[qb] += lp[qb];
+        };
 
-        // Some p > 2^kTau (or +inf) means the running max is too low for this
-        // tile: take the exact max of the scores, rescale O and l, and redo P.
-        // The branch is per wave, so it stays uniform.
-        const float pmax = fmaxf((float)pm[0], (float)pm[1]);
-        if (__builtin_expect(__any(pmax > kPmaxLimit), 0)) {
-            float mx = -INFINITY;
+        f32x16 Sa[QB], Sb[QB];
+        f16x8 Pa[QB][2], Pb[QB][2];
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-                for (int r = 0; r < 16; r += 2) mx = max3(mx, S[kb][r], S[kb][r + 1]);
-            mx = half_swap_max(mx) * c;
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-            for (int b = 0; b < NOB; ++b) oacc[b] *= alpha;
-            l_run *= alpha;
-            m_run = m_new;
-            l_tile = 0.f;
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-                block_exp(S[kb], P[2 * kb], P[2 * kb + 1], -m_run, l_tile, pm);
-        }
-        l_run += l_tile;
+            for (int ks = 0; ks < 2; ++ks) Pb[qb][ks] = f16x8{};  // block -1: no keys
 
-        // O^T += V^T P^T.
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-            for (int b = 0; b < NOB; ++b) {
-                const int off = ks * 16 * RB + (b & ~3) * 64;
-                const f16x4 lo = lds_read_tr(sv, vaddr[b & 3] + off);
-                const f16x4 hi = lds_read_tr(sv, vaddr[b & 3] + off + 8 * RB);
-                const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                oacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[ks], oacc[b], 0, 0, 0);
-            }
-        if constexpr (C::INTERLEAVE) {
-            // Two transposed reads ahead per MFMA instead of all of them.
-            constexpr int N = NKS * NOB;
-            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
-#pragma unroll
-            for (int i = 0; i < N - 2; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
-        }
-    };
+        // Tile w (blocks 2w, 2w+1) in stage cur; prev holds tile w-1, nxt
+        // tile w+1; fill (the stage of tile w-1) takes tile w+3.
+        auto tile = [&](int w, const char* prev, const char* cur, const char* nxt, char* fill)
+                __attribute__((always_inline)) {
+            mask(Sa, w * C::BN);
+            pv(prev, 1, Pb);   // block 2w-1
+            qk(cur, 1, Sb);    // block 2w+1
+            softmax(Sa, Pa);   // block 2w
+            __builtin_amdgcn_s_waitcnt(kWaitNext);  // own loads of tile w+1 done
+            __syncthreads();                        // every wave's; tile w-1 consumed
+            issue(w + 3, fill);
+            mask(Sb, w * C::BN + 32);
+            pv(cur, 0, Pa);    // block 2w
+            qk(nxt, 0, Sa);    // block 2w+2
+            softmax(Sb, Pb);   // block 2w+1
+        };
 
-    // Own loads of tile t complete, then every wave's: tile t is in LDS and
-    // all waves are done with tile t-1, whose stage the next loads reuse.
-    auto step = [&](int t, auto masked) __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        // Prologue: tiles 0 and 1 in flight, stage 3's V zeroed for the PV
+        // of block -1 (P = 0, and 0 * garbage could be NaN), tile 2 issued
+        // once tile 0 is in, then S of block 0.
+        issue(0, st0);
+        issue(1, st1);
+        for (int i = tid; i < TILE / 16; i += C::NT)
+            *reinterpret_cast<u32x4*>(st3 + TILE + 16 * i) = u32x4{};
+        __builtin_amdgcn_s_waitcnt(kWaitNext);
         __syncthreads();
-        tile(t, masked, stage(t + 1), stage(t));
-    };
-    const int nfull = Skv / BN;  // tiles with no key past Skv
-    for (int t = 0; t < nfull; ++t) step(t, std::false_type{});
-    if (nfull < ntiles) step(nfull, std::true_type{});
+        issue(2, st2);
+        qk(st0, 0, Sa);
 
-    const float l = half_swap_sum(l_run);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (live) {
-        f16* op = Oh + (long)qrow * D;
+        // Tile w sits in stage w % 4. The loop runs whole groups of four
+        // tiles: tiles past the end hold zeros and are masked to p = 0 (at
+        // most three per workgroup). A single exit keeps the register
+        // allocation of the loop body intact; exits after each tile do not.
+        for (int w0 = 0;; w0 += 4) {
+            tile(w0 + 0, st3, st0, st1, st3);
+            tile(w0 + 1, st0, st1, st2, st0);
+            tile(w0 + 2, st1, st2, st3, st1);
+            tile(w0 + 3, st2, st3, st0, st2);
+            if (w0 + 4 >= ntiles) break;
+        }
+        pv(st3, 1, Pb);  // block 2w+1 of the last tile
+        // The zero-range loads past the end must land before the workgroup's
+        // LDS is released.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+
 #pragma unroll
-        for (int b = 0; b < NOB; ++b)
+    for (int qb = 0; qb < QB; ++qb) {
+        const int row = qrow0 + 32 * qb;
+        const float l = half_swap_sum(l_run[qb]);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        if (row < Sq) {
+            f16* op = Oh + (long)row * D;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int d0 = 32 * b + 8 * rr + 4 * g;
-                if (!PAD || d0 < D) {
-                    const f16x2 h0 = __builtin_convertvector(
-                        f32x2{oacc[b][4 * rr + 0] * inv, oacc[b][4 * rr + 1] * inv}, f16x2);
-                    const f16x2 h1 = __builtin_convertvector(
-                        f32x2{oacc[b][4 * rr + 2] * inv, oacc[b][4 * rr + 3] * inv}, f16x2);
-                    const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
-                    *reinterpret_cast<f16x4*>(op + d0) = h;
+            for (int b = 0; b < NOB; ++b)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int d0 = 32 * b + 8 * rr + 4 * g;
+                    if (!PAD || d0 < D) {
+                        const f16x2 h0 = __builtin_convertvector(
+                            f32x2{oacc[qb][b][4 * rr + 0] * inv, oacc[qb][b][4 * rr + 1] * inv}, f16x2);
+                        const f16x2 h1 = __builtin_convertvector(
+                            f32x2{oacc[qb][b][4 * rr + 2] * inv, oacc[qb][b][4 * rr + 3] * inv}, f16x2);
+                        const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
+                        *reinterpret_cast<f16x4*>(op + d0) = h;
+                    }
                 }
-            }
+        }
     }
 #endif
 }
@@ -678,15 +722,6 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
 
 // Tile configurations per head-dim class (waves per workgroup, keys per
 // tile, waves per SIMD); the macros exist for tuning sweeps.
-#ifndef ATTN_CFG64
-#define ATTN_CFG64 8, 64, 2
-#endif
-#ifndef ATTN_CFG128
-#define ATTN_CFG128 8, 128, 2
-#endif
-using Cfg64 = Cfg<64, ATTN_CFG64>;
-using Cfg128 = Cfg<128, ATTN_CFG128>;
-
 thread_local char g_err[256];
 
 void set_err(const char* msg) {
@@ -695,18 +730,17 @@ void set_err(const char* msg) {
     g_err[i] = 0;
 }
 
+using Cfg128 = Cfg<128, 8, 1, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
+using Cfg64 = Cfg<64, 8, 1, 2>;    // 64 KB: two workgroups, four waves per SIMD
+
 template <class C, bool PAD>
-hipError_t launch_cfg(const void* q, const void* k, const void* v, void* o, int B, int H,
+hipError_t launch_pipe(const void* q, const void* k, const void* v, void* o, int B, int H,
                       int Sq, int Skv, int D, float scale, hipStream_t s) {
     dim3 grid((unsigned)((Sq + C::BM - 1) / C::BM) * (unsigned)(B * H));
-    // Masked keys carry score -inf and rely on c > 0 (-inf * 0 is NaN). For
-    // scale == 0, c = 1e-30 gives exp2(s*c - m) == 1.0f exactly for every
-    // finite score, i.e. the same uniform weights as c == 0.
-    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
+    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);  // see launch_cfg
     const float qsign = scale < 0.f ? -1.f : 1.f;
-    hipLaunchKernelGGL((attn_fwd_mfma<C, PAD>), grid, dim3(C::NT), 0, s,
-                       (const f16*)q, (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, D, c,
-                       qsign);
+    hipLaunchKernelGGL((attn_fwd_pipe<C, PAD>), grid, dim3(C::NT), 0, s, (const f16*)q,
+                       (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, D, c, qsign);
     return hipGetLastError();
 }
 
@@ -720,13 +754,11 @@ hipError_t launch_d512(const void* q, const void* k, const void* v, void* o, int
     return hipGetLastError();
 }
 
-}  // namespace
-
-extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr; }
-
-extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,
-                        int Sq, int Skv, int D, float scale, hipStream_t s) {
-    g_err[0] = 0;
+// Validates the arguments; returns 0 and the workspace size, or 1 with the
+// error message set.
+// Validates the arguments; returns 0, or 1 with the error message set.
+int check_args(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
+               int Skv, int D) {
     if (B < 0 || H < 0 || Sq < 0 || Skv < 0) {
         set_err("attn: negative size");
         return 1;
@@ -735,7 +767,7 @@ extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, in
         set_err("attn: head_dim must be <=64 and a multiple of 8, or 128, or 512");
         return 1;
     }
-    if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL) {
+    if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL || (long)B * H > 65535) {
         set_err("attn: grid too large");
         return 1;
     }
@@ -744,20 +776,37 @@ extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, in
         set_err("attn: null pointer");
         return 1;
     }
+    return 0;
+}
+
+int run(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq, int Skv,
+        int D, float scale, hipStream_t s) {
     hipError_t e;
     if (D == 128)
-        e = launch_cfg<Cfg128, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+        e = launch_pipe<Cfg128, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
     else if (D == 64)
-        e = launch_cfg<Cfg64, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+        e = launch_pipe<Cfg64, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
     else if (D == 512)
         e = launch_d512(q, k, v, o, B, H, Sq, Skv, scale, s);
     else
-        e = launch_cfg<Cfg64, true>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+        e = launch_pipe<Cfg64, true>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;
     }
     return 0;
+}
+
+}  // namespace
+
+extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr; }
+
+extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,
+                        int Sq, int Skv, int D, float scale, hipStream_t s) {
+    g_err[0] = 0;
+    if (check_args(q, k, v, o, B, H, Sq, Skv, D)) return 1;
+    if (B == 0 || H == 0 || Sq == 0) return 0;
+    return run(q, k, v, o, B, H, Sq, Skv, D, scale, s);
 }
 
 extern "C" void launch(const void* q, const void* k, const void* v, void* o, int B, int H,
