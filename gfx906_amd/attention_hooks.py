@@ -10,9 +10,11 @@ with the same caller contract:
 * :func:`container_attn` takes the kernel path for eligible calls (:func:`eligible`,
   reference :38-49: no mask or GQA, fp16/bf16 CUDA 4-D tensors with equal B, H
   and D, ``k.shape == v.shape``, ``H == heads``, D in {128, 512} or D <= 64 and a
-  multiple of 8, and ``skip_reshape=True``), casts bf16 to fp16 and back
-  (:71-75), and returns ``[B, S, H*D]`` unless ``skip_output_reshape`` (:76-79).
-  Anything else goes to the stock callable unchanged (:58-62).
+  multiple of 8, and ``skip_reshape=True``) and returns ``[B, S, H*D]`` unless
+  ``skip_output_reshape`` (:76-79). Where the reference casts bf16 to fp16 and
+  back around its kernel (:71-75), bf16 runs natively here, and the
+  ``[B, S, H*D]`` result is written by the kernel in that layout (no transpose
+  copy). Anything else goes to the stock callable unchanged (:58-62).
 * :func:`vae_attn` serves the VAE mid-block attention (``[b, c, h, w]``,
   c = 512) as one ``[b, 1, h*w, c]`` attention and falls back to the
   function the factory selected if the kernel raises (:82-111);
@@ -68,15 +70,6 @@ def eligible(qt, kt, vt, heads, mask, kwargs) -> bool:
     return head_dim_supported(qt.shape[3])
 
 
-def _run_fp16(mod, q, k, v, scale):
-    """Kernel call with bf16 inputs cast to fp16 and the result cast back."""
-    out_dtype = q.dtype
-    if out_dtype != torch.float16:
-        q, k, v = q.half(), k.half(), v.half()
-    out = mod.attn(q, k, v, scale)
-    return out if out_dtype == torch.float16 else out.to(out_dtype)
-
-
 def container_attn(q, k, v, heads, mask=None, attn_precision=None, skip_reshape=False,
                    skip_output_reshape=False, **kwargs):
     """``container_function`` for ``optimized_attention``: q/k/v are containers
@@ -96,11 +89,12 @@ def container_attn(q, k, v, heads, mask=None, attn_precision=None, skip_reshape=
     scale = kwargs.get("scale")
     if scale is None:
         scale = qt.shape[-1] ** -0.5  # SDPA's default
-    out = _run_fp16(mod, qt, kt, vt, scale)
     if skip_output_reshape:
-        return out
-    b, h, s, d = out.shape
-    return out.transpose(1, 2).reshape(b, s, h * d)
+        return mod.attn(qt, kt, vt, scale)
+    b, h, s, d = qt.shape
+    out = torch.empty((b, s, h, d), dtype=qt.dtype, device=qt.device)
+    mod.attn(qt, kt, vt, scale, out=out.transpose(1, 2))
+    return out.view(b, s, h * d)
 
 
 def vae_attn(q, k, v, fallback):
@@ -118,11 +112,12 @@ def vae_attn(q, k, v, fallback):
         return fallback(q, k, v)
     b, c, h, w = q.shape
 
-    def tokens(x):  # [b, c, h, w] -> [b, 1, h*w, c] (a view; the binding copies it)
+    def tokens(x):  # [b, c, h, w] -> [b, 1, h*w, c]: a view with strided channels,
+        # which the binding copies (the kernel reads a contiguous head dim)
         return x.reshape(b, c, h * w).transpose(1, 2).unsqueeze(1)
 
     try:
-        out = _run_fp16(mod, tokens(q), tokens(k), tokens(v), c ** -0.5)
+        out = mod.attn(tokens(q), tokens(k), tokens(v), c ** -0.5)
     except Exception:  # noqa: BLE001 - a VAE decode must not fail on the fast path
         logger.warning("gfx950 VAE attention failed; using %s",
                        getattr(fallback, "__name__", fallback))

@@ -1,27 +1,69 @@
-// PyTorch binding for the gfx950 attention forward: attn(q, k, v, scale).
+// PyTorch binding for the gfx950 attention forward: attn(q, k, v, scale, out=None).
 //
 // Same Python signature, accept/reject set and ownership as the reference
-// binding (attn.cpp:6-21): fp16 CUDA q/k/v of shape [B, H, S, D] with equal B,
-// H and D, k.shape == v.shape, D <= 64 and a multiple of 8, or 128, or 512.
-// Non-contiguous inputs are copied to contiguous ones; the output is a new
-// contiguous [B, H, Sq, D] fp16 tensor on q's device. The kernel runs on the
-// current HIP stream and the call returns without synchronising.
+// binding (attn.cpp:6-21) for its fp16 case: CUDA q/k/v of shape [B, H, S, D]
+// with equal B, H and D, k.shape == v.shape, D <= 64 and a multiple of 8, or
+// 128, or 512. The output is a new contiguous [B, H, Sq, D] tensor of q's
+// dtype on q's device. The kernel runs on the current HIP stream and the call
+// returns without synchronising.
 //
-// Checks the reference binding lacks, all raising RuntimeError: k and v must
-// be fp16 on q's device, sizes must fit the kernel's 32-bit indexing, and a
-// launch error is reported instead of being dropped.
+// Beyond the reference binding:
+//  * bf16 q/k/v run natively (bf16 MFMA), with a bf16 output; the reference
+//    accepts fp16 only and its hook casts bf16 around it
+//    (deploy/gfx906_attention.py:71-75).
+//  * Strided inputs are read in place when the head dim is contiguous and
+//    the other strides are multiples of 8 elements (16-byte aligned data);
+//    only other layouts are copied, where the reference always calls
+//    .contiguous() (attn.cpp:15).
+//  * `out`, if given, is written instead of allocating: any [B, H, Sq, D]
+//    view of q's dtype and device with a contiguous head dim and
+//    non-overlapping rows, e.g. the transpose of a [B, Sq, H, D] buffer. It
+//    must not overlap k or v (every workgroup of a head reads them); it may
+//    be q itself (a workgroup reads its own query rows before writing them).
+//  * Checks raising RuntimeError: k and v must match q's dtype and device,
+//    sizes must fit the kernel's indexing, and a launch error is reported
+//    instead of being dropped.
 #include <torch/extension.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
 
 #include "gfx906_amd_attn.h"
 
-torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double scale) {
-    TORCH_CHECK(q.is_cuda() && q.dtype() == torch::kHalf, "kernel: q must be a CUDA fp16 tensor");
+namespace {
+
+// Element strides {batch, head, seq} of a 4-D tensor (0 for size-1 dims,
+// whose stride is never used).
+std::array<long long, 3> strides3(const torch::Tensor& t) {
+    std::array<long long, 3> s;
+    for (int d = 0; d < 3; ++d) s[d] = t.size(d) == 1 ? 0 : t.stride(d);
+    return s;
+}
+
+// Whether the kernel can read t in place: contiguous head dim, non-negative
+// strides that are multiples of 8 elements, 16-byte aligned data, and (for
+// k and v) a sequence stride the 32-bit tile offsets can hold.
+bool readable_in_place(const torch::Tensor& t, bool kv) {
+    if (t.stride(3) != 1) return false;
+    if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) return false;
+    for (long long s : strides3(t))
+        if (s < 0 || s % 8) return false;
+    return !kv || strides3(t)[2] <= (1 << 24);
+}
+
+torch::Tensor as_input(const torch::Tensor& t, bool kv) {
+    return readable_in_place(t, kv) ? t : t.clone(at::MemoryFormat::Contiguous);
+}
+
+}  // namespace
+
+torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double scale,
+                   c10::optional<torch::Tensor> out) {
+    TORCH_CHECK(q.is_cuda() && (q.dtype() == torch::kHalf || q.dtype() == torch::kBFloat16),
+                "kernel: q must be a CUDA fp16 or bf16 tensor");
     TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
                 "kernel: q, k and v must be on the same device");
-    TORCH_CHECK(k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
-                "kernel: k and v must be fp16");
+    TORCH_CHECK(k.dtype() == q.dtype() && v.dtype() == q.dtype(),
+                "kernel: k and v must have q's dtype");
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "kernel: q/k/v must be 4-D [B,H,S,D]");
     const c10::DeviceGuard guard(q.device());
     TORCH_CHECK(k.sizes() == v.sizes() && q.size(0) == k.size(0) && q.size(1) == k.size(1) &&
@@ -33,16 +75,32 @@ torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double sca
     TORCH_CHECK(B * H * std::max<int64_t>(Sq, Skv) * D < (int64_t(1) << 40) && Sq < (1 << 30) &&
                     Skv < (1 << 30) && B * H < (1 << 30),
                 "kernel: tensor too large");
-    auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
-    auto o = torch::empty_like(qc, qc.options().memory_format(at::MemoryFormat::Contiguous));
+    torch::Tensor o;
+    if (out.has_value()) {
+        o = *out;
+        TORCH_CHECK(o.device() == q.device() && o.dtype() == q.dtype(),
+                    "kernel: out must have q's dtype and device");
+        TORCH_CHECK(o.dim() == 4 && o.size(0) == B && o.size(1) == H && o.size(2) == Sq &&
+                        o.size(3) == D,
+                    "kernel: out must be [B, H, Sq, D]");
+        TORCH_CHECK(o.stride(3) == 1, "kernel: out must have a contiguous head dim");
+    } else {
+        o = torch::empty({B, H, Sq, D}, q.options().memory_format(at::MemoryFormat::Contiguous));
+    }
     if (o.numel() == 0) return o;
-    const int rc = attn_fwd(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), (int)B,
-                            (int)H, (int)Sq, (int)Skv, (int)D, (float)scale,
-                            c10::hip::getCurrentHIPStream().stream());
+    const auto qi = as_input(q, false), ki = as_input(k, true), vi = as_input(v, true);
+    const auto sq = strides3(qi), sk = strides3(ki), sv = strides3(vi), so = strides3(o);
+    const int dtype = q.dtype() == torch::kBFloat16 ? ATTN_DTYPE_BF16 : ATTN_DTYPE_F16;
+    const int rc = attn_fwd_ex(qi.data_ptr(), ki.data_ptr(), vi.data_ptr(), o.data_ptr(), (int)B,
+                               (int)H, (int)Sq, (int)Skv, (int)D, (float)scale,
+                               c10::hip::getCurrentHIPStream().stream(), dtype, sq.data(),
+                               sk.data(), sv.data(), so.data());
     TORCH_CHECK(rc == 0, "kernel: ", attn_last_error() ? attn_last_error() : "launch failed");
     return o;
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.def("attn", &attn, "fp16 attention forward on gfx950 (q, k, v, scale)");
+    m.def("attn", &attn, "fp16/bf16 attention forward on gfx950 (q, k, v, scale, out=None)",
+          pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("scale"),
+          pybind11::arg("out") = pybind11::none());
 }

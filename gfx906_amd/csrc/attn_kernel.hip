@@ -1,21 +1,23 @@
-// Flash-attention forward for AMD MI355X (gfx950 / CDNA4), fp16 in/out.
+// Flash-attention forward for AMD MI355X (gfx950 / CDNA4), fp16 or bf16 in/out.
 //
 // Computes, per (batch, head) and query row i:
 //     o_i = sum_j softmax_j(scale * <q_i, k_j>) * v_j
-// on contiguous [B, H, S, D] tensors with Sq != Skv allowed, no mask, no dropout.
-// This is the computation behind the reference's `launch` entry point
+// on [B, H, S, D] tensors (any batch / head / sequence strides, unit stride
+// along D) with Sq != Skv allowed, no mask, no dropout. This is the
+// computation behind the reference's `launch` entry point
 // (attn_kernel.hip:710-742, dispatch) and its per-D kernels
 // (attn_pair_gfx906 attn_kernel.hip:313-512 for D=64/128, attn_d512_gfx906
 // attn_kernel.hip:525-708 for D=512, attn_tiled_gfx906 attn_kernel.hip:146-308
-// for D<64). The reference kernels run on VALU dot2 instructions; this file
-// is a different design built around CDNA4 matrix cores:
+// for D<64). The reference kernels run on VALU dot2 instructions over
+// contiguous fp16; this file is a different design built around CDNA4 matrix
+// cores:
 //
 //  * Scores are computed transposed, S^T = K * Q^T, with
-//    v_mfma_f32_32x32x16_f16. In the 32x32 accumulator layout a lane holds one
-//    column (one query row) and 16 of the 32 keys of a key block, so the
-//    online-softmax state (running max m, running sum l) is a per-lane scalar
-//    and the row reductions need a single exchange with lane^32.
-//  * The same registers, rounded to fp16, are the B operand of
+//    v_mfma_f32_32x32x16_{f16,bf16}. In the 32x32 accumulator layout a lane
+//    holds one column (one query row) and 16 of the 32 keys of a key block, so
+//    the online-softmax state (running max m, running sum l) is a per-lane
+//    scalar and the row reductions need a single exchange with lane^32.
+//  * The same registers, rounded to the input type, are the B operand of
 //    O^T = V^T * P^T. V stays row-major ([key][dim]) in LDS and the A operand
 //    is read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane
 //    four keys of one dim; the key order is chosen to match the accumulator
@@ -33,11 +35,11 @@
 //    row sum of p = exp2(s*c - m) exceeds 2^15 (the block's max rose well
 //    above the running max, or this is the first block), which keeps every p
 //    finite in fp16 and skips the rescale on almost every block.
-//  * The row sum l is accumulated from the fp16-rounded P (v_dot2_f32_f16
+//  * The row sum l is accumulated from the rounded P (v_dot2_f32_{f16,bf16}
 //    against 1.0), so numerator and denominator see the same rounded weights.
-//  * Output rows are normalised by 1/l and rounded to fp16 (RNE), as the
-//    reference does (attn_kernel.hip:497-511). Rows of a head with Skv == 0
-//    are written as zeros (the reference leaves them unwritten).
+//  * Output rows are normalised by 1/l and rounded to the input type (RNE),
+//    as the reference does for fp16 (attn_kernel.hip:497-511). Rows of a head
+//    with Skv == 0 are written as zeros (the reference leaves them unwritten).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
@@ -48,17 +50,21 @@
 namespace {
 
 typedef _Float16 f16;
+typedef __bf16 bf16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
-#define GLOBAL_AS __attribute__((address_space(1)))
 
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy rescale: a block whose lane row sum exceeds this takes the exact max.
@@ -69,8 +75,70 @@ constexpr float kPmaxLimit = 256.0f;  // 2^kTau
 // sched_group_barrier instruction classes
 constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
 
-__device__ __forceinline__ f16x8 ld_global16(const f16* p) {
-    return *reinterpret_cast<const f16x8*>(p);
+// Strides of one tensor in elements: batch, head, sequence (the head dim is
+// contiguous).
+struct Strides3 {
+    long long b, h, s;
+};
+
+// Kernel arguments. c = |scale| * log2(e) (at least 1e-30); qsign < 0 for a
+// negative scale, applied as negated q.
+struct KArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    Strides3 sq, sk, sv, so;
+    int H, Sq, Skv, D;
+    float c, qsign;
+};
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Per-element-type operations: vectors, MFMAs, packed RNE conversion from
+// fp32 and a dot2 against (1, 1) accumulating in fp32.
+template <class T>
+struct Elem;
+template <>
+struct Elem<f16> {
+    using x8 = f16x8;
+    using x4 = f16x4;
+    using x2 = f16x2;
+    static __device__ __forceinline__ f32x16 mma32(x8 a, x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ x2 cvt2(float a, float b) {
+        return __builtin_convertvector(f32x2{a, b}, x2);
+    }
+    static __device__ __forceinline__ float sum2(x2 h, float acc) {
+        return __builtin_amdgcn_fdot2(h, x2{(f16)1.0f, (f16)1.0f}, acc, false);
+    }
+};
+template <>
+struct Elem<bf16> {
+    using x8 = bf16x8;
+    using x4 = bf16x4;
+    using x2 = bf16x2;
+    static __device__ __forceinline__ f32x16 mma32(x8 a, x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ x2 cvt2(float a, float b) {
+        return __builtin_convertvector(f32x2{a, b}, x2);
+    }
+    static __device__ __forceinline__ float sum2(x2 h, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(h, x2{(bf16)1.0f, (bf16)1.0f}, acc, false);
+    }
+};
+
+// 16-byte global load of 8 elements.
+template <class T>
+__device__ __forceinline__ typename Elem<T>::x8 ld_global16(const T* p) {
+    return *reinterpret_cast<const typename Elem<T>::x8*>(p);
 }
 
 // Three-way max; with NaN-free arithmetic assumed (-fno-honor-nans) the
@@ -80,70 +148,25 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 }
 
 // 16-byte LDS read at a byte address.
-__device__ __forceinline__ f16x8 lds_read16(const char* base, int byte_off) {
-    return *(const LDS_AS f16x8*)((const LDS_AS char*)base + byte_off);
+template <class T>
+__device__ __forceinline__ typename Elem<T>::x8 lds_read16(const char* base, int byte_off) {
+    return *(const LDS_AS typename Elem<T>::x8*)((const LDS_AS char*)base + byte_off);
 }
-// Transposed 8-byte LDS read (see the 16-lane mapping in the header comment).
-__device__ __forceinline__ f16x4 lds_read_tr(const char* base, int byte_off) {
-    fp16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-        (LDS_AS fp16x4_t*)((LDS_AS char*)base + byte_off));
-    return __builtin_bit_cast(f16x4, r);
-}
-
-// XOR swizzles of the 16-byte unit index within a row.
-//  K: the QK^T read takes one unit from 32 consecutive rows, so 16
-//     consecutive rows must land on 16 different bank groups.
-//  V: the transposed read takes 4 units from 8 consecutive rows; each half
-//     wave (4 rows x 4 units) must cover all 16 bank groups.
-template <int NU>
-__device__ __forceinline__ int kswz(int r) { return NU >= 16 ? (r & 15) : ((r >> 1) & 7); }
-template <int NU>
-__device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
-
-// Per-lane byte offsets of the direct HBM->LDS tile loads. Each wave fills
-// whole 1 KB LDS blocks (lane i writes 16-byte unit i of its block) for
-// BLKS/NW blocks of each K tile and as many of each V tile. The offsets are
-// relative to the tile's first row and do not change from tile to tile.
-// Units past D (padded head dims) are pointed at unit 0 of the row: finite
-// data that meets zero Q columns (K) or feeds unused output columns (V).
-template <class C, bool PAD>
-__device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
-                                             int (&voff)[C::BLKS / C::NW], int D, int wave,
-                                             int lane) {
-#pragma unroll
-    for (int i = 0; i < C::BLKS / C::NW; ++i) {
-        const int unit = (wave + i * C::NW) * 64 + lane;
-        const int row = unit / C::NU, slot = unit % C::NU;
-        int ck = slot ^ kswz<C::NU>(row);
-        if (PAD && ck * 8 >= D) ck = 0;
-        koff[i] = (row * D + ck * 8) * 2;
-        int cv = slot ^ vswz<C::NU>(row);
-        if (PAD && cv * 8 >= D) cv = 0;
-        voff[i] = (row * D + cv * 8) * 2;
-    }
+// Two transposed 8-byte LDS reads (ds_read_b64_tr_b16: within each 16-lane
+// group, lane i gets element i%4 of the 8 bytes read by lanes 4e+i/4) joined
+// into one MFMA operand. The read moves 16-bit elements whatever their type.
+template <class T>
+__device__ __forceinline__ typename Elem<T>::x8 lds_read_tr2(const char* base, int lo_off,
+                                                              int hi_off) {
+    const fp16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (LDS_AS fp16x4_t*)((LDS_AS char*)base + lo_off));
+    const fp16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (LDS_AS fp16x4_t*)((LDS_AS char*)base + hi_off));
+    const u32x2 l = __builtin_bit_cast(u32x2, lo), h = __builtin_bit_cast(u32x2, hi);
+    return __builtin_bit_cast(typename Elem<T>::x8, u32x4{l[0], l[1], h[0], h[1]});
 }
 
-#if defined(__HIP_DEVICE_COMPILE__)
-// Issue the loads of one K (or V) tile starting at key n0 into an LDS stage.
-// The buffer descriptor covers exactly the tile's valid rows, so rows past
-// Skv read as zeros and nothing outside the tensor is touched; a tile that
-// starts at or past Skv has an empty range and fills the stage with zeros.
-template <class C>
-__device__ __forceinline__ void issue_tile(const f16* __restrict__ X, int n0, int Skv, int D,
-                                           char* stage, int wave,
-                                           const int (&off)[C::BLKS / C::NW]) {
-    // Uniform; readfirstlane keeps the descriptor in SGPRs (a clamp selected
-    // as a VALU op would otherwise force a waterfall loop around each load).
-    const int bytes = __builtin_amdgcn_readfirstlane(max(0, min(Skv - n0, C::BN)) * D * 2);
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(X + (long)n0 * D), 0, bytes, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < C::BLKS / C::NW; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)(stage + (wave + i * C::NW) * 1024),
-                                                 16, off[i], 0, 0, 0);
-}
-
-// Max of x over lanes l and l^32 (both halves get the result).
+// Max / sum of x over lanes l and l^32 (both halves get the result).
 __device__ __forceinline__ float half_swap_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                     false);
@@ -155,22 +178,51 @@ __device__ __forceinline__ float half_swap_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sum / max over lanes i, i+16, i+32, i+48.
+__device__ __forceinline__ float quad_group_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float quad_group_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Q^T fragment: 8 elements of a query row with the sign flipped for a
+// negative scale (exact for fp16 and bf16 alike: bit 15 of each element).
+template <class T>
+__device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load, unsigned qneg) {
+    typename Elem<T>::x8 val = {};
+    if (load) val = ld_global16(p);
+    return __builtin_bit_cast(typename Elem<T>::x8, __builtin_bit_cast(u32x4, val) ^ qneg);
+}
+
 // P for one 32-key block of S^T (a lane's 16 scores, two 16-key PV steps):
-// p = exp2(s*c + nm) rounded to fp16, nm = -(running max). Adds the block's
-// row-sum contribution, taken from the fp16-rounded values, to lsum.
-__device__ __forceinline__ void block_exp_f16(const f32x16& Sb, f16x8& P0, f16x8& P1, float nm,
-                                              float c, float& lsum) {
+// p = exp2(s*c + nm) rounded to the element type, nm = -(running max). Adds
+// the block's row-sum contribution, taken from the rounded values, to lsum.
+template <class T>
+__device__ __forceinline__ void block_exp(const f32x16& Sb, typename Elem<T>::x8& P0,
+                                          typename Elem<T>::x8& P1, float nm, float c,
+                                          float& lsum) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        f16x8& P = h ? P1 : P0;
+        typename Elem<T>::x8& P = h ? P1 : P0;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e], c, nm));
             const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 1], c, nm));
-            const f16x2 hp = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+            const typename Elem<T>::x2 hp = Elem<T>::cvt2(p0, p1);
             P[e] = hp[0];
             P[e + 1] = hp[1];
-            lsum = __builtin_amdgcn_fdot2(hp, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+            lsum = Elem<T>::sum2(hp, lsum);
         }
     }
 }
@@ -183,6 +235,16 @@ __device__ __forceinline__ bool needs_rescale(float lsum) {
     return __any(!(lsum <= kLsumLimit));
 }
 #endif
+
+// XOR swizzles of the 16-byte unit index within a row.
+//  K: the QK^T read takes one unit from 32 consecutive rows, so 16
+//     consecutive rows must land on 16 different bank groups.
+//  V: the transposed read takes 4 units from 8 consecutive rows; each half
+//     wave (4 rows x 4 units) must cover all 16 bank groups.
+template <int NU>
+__device__ __forceinline__ int kswz(int r) { return NU >= 16 ? (r & 15) : ((r >> 1) & 7); }
+template <int NU>
+__device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 
 // ---------------------------------------------------------------------------
 // D <= 128: software-pipelined waves, 32 * QB query rows each.
@@ -211,7 +273,7 @@ struct Cfg {
     static constexpr int BM = NW * 32 * QB;     // query rows per workgroup
     static constexpr int NT = NW * 64;          // threads per workgroup
     static constexpr int NU = DP / 8;           // 16-byte units per row
-    static constexpr int RB = DP * 2;           // bytes per row
+    static constexpr int RB = DP * 2;           // bytes per LDS row
     static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
     static constexpr int STAGE = 2 * TILE;      // K tile, then V tile
     static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
@@ -219,15 +281,62 @@ struct Cfg {
     static_assert(DP % 32 == 0 && DP <= 128, "head-dim class");
 };
 
+// Per-lane byte offsets of the direct HBM->LDS tile loads. Each wave fills
+// whole 1 KB LDS blocks (lane i writes 16-byte unit i of its block) for
+// BLKS/NW blocks of each K tile and as many of each V tile. The offsets are
+// relative to the tile's first row (rows kss / vss elements apart in HBM)
+// and do not change from tile to tile. Units past D (padded head dims) are
+// pointed at unit 0 of the row: finite data that meets zero Q columns (K) or
+// feeds unused output columns (V).
+template <class C, bool PAD>
+__device__ __forceinline__ void tile_offsets(int (&koff)[C::BLKS / C::NW],
+                                             int (&voff)[C::BLKS / C::NW], int D, int kss,
+                                             int vss, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < C::BLKS / C::NW; ++i) {
+        const int unit = (wave + i * C::NW) * 64 + lane;
+        const int row = unit / C::NU, slot = unit % C::NU;
+        int ck = slot ^ kswz<C::NU>(row);
+        if (PAD && ck * 8 >= D) ck = 0;
+        koff[i] = (row * kss + ck * 8) * 2;
+        int cv = slot ^ vswz<C::NU>(row);
+        if (PAD && cv * 8 >= D) cv = 0;
+        voff[i] = (row * vss + cv * 8) * 2;
+    }
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Issue the loads of one K (or V) tile starting at key n0 into an LDS stage
+// (rows ss elements apart). The buffer descriptor covers exactly the tile's
+// valid rows, so rows past Skv read as zeros and nothing outside the tensor
+// is touched; a tile that starts at or past Skv has an empty range and fills
+// the stage with zeros.
+template <class C, class T>
+__device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int Skv, int D,
+                                           long long ss, char* stage, int wave,
+                                           const int (&off)[C::BLKS / C::NW]) {
+    const int rows = max(0, min(Skv - n0, C::BN));
+    // Uniform; readfirstlane keeps the descriptor in SGPRs (a clamp selected
+    // as a VALU op would otherwise force a waterfall loop around each load).
+    const int bytes =
+        __builtin_amdgcn_readfirstlane(rows > 0 ? (int)(((rows - 1) * ss + D) * 2) : 0);
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(X + n0 * ss), 0, bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < C::BLKS / C::NW; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)(stage + (wave + i * C::NW) * 1024),
+                                                 16, off[i], 0, 0, 0);
+}
+#endif
+
 // grid: ceil(Sq / BM) * B*H workgroups, query tiles of one head adjacent;
 // block: NW*64 threads.
-
-template <class C, bool PAD>
+template <class C, bool PAD, class T>
 __global__ void __launch_bounds__(C::NT, C::OCC)
-attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
-             const f16* __restrict__ V, f16* __restrict__ O,
-             int Sq, int Skv, int D, float c, float qsign) {
+attn_fwd_pipe(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
+    using E = Elem<T>;
+    using x8 = typename E::x8;
     constexpr int DP = C::DP, NU = C::NU, RB = C::RB, TILE = C::TILE, QB = C::QB;
     constexpr int NQF = DP / 16;  // Q fragments (16 dims each) per query block
     constexpr int NOB = DP / 32;  // 32-dim output blocks
@@ -239,32 +348,33 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
     __shared__ __attribute__((aligned(1024))) char st2[C::STAGE];
     __shared__ __attribute__((aligned(1024))) char st3[C::STAGE];
 
+    const int Sq = a.Sq, Skv = a.Skv, D = a.D;
+    const float c = a.c;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, r32 = lane & 31;
     const int j16 = lane & 15, G = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    const long bh = blockIdx.x / nqt;
+    const int bh = blockIdx.x / nqt;
     const int qt = blockIdx.x % nqt;
-    const f16* Qh = Q + bh * (long)Sq * D;
-    const f16* Kh = K + bh * (long)Skv * D;
-    const f16* Vh = V + bh * (long)Skv * D;
-    f16* Oh = O + bh * (long)Sq * D;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+    T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
     const int qrow0 = qt * C::BM + wave * 32 * QB + r32;  // this lane's rows: qrow0 + 32 qb
     const int ntiles = (Skv + C::BN - 1) / C::BN;
 
     // Q^T fragments (B operands), loaded before any tile so that the tile
-    // waits below also cover them. Negative scale: sign bits flipped.
-    f16x8 qf[QB][NQF];
-    const unsigned qneg = qsign < 0.f ? 0x80008000u : 0u;
+    // waits below also cover them.
+    x8 qf[QB][NQF];
+    const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int s = 0; s < NQF; ++s) {
             const int d0 = 16 * s + 8 * g, row = qrow0 + 32 * qb;
-            f16x8 val = {};
-            if (row < Sq && (!PAD || d0 < D)) val = ld_global16(Qh + (long)row * D + d0);
-            qf[qb][s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
+            qf[qb][s] = q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
         }
 
     f32x16 oacc[QB][NOB];
@@ -272,7 +382,7 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
-        for (int b = 0; b < NOB; ++b) oacc[qb][b] = f32x16{};
+        for (int ob = 0; ob < NOB; ++ob) oacc[qb][ob] = f32x16{};
         // Running max in units of s*c (log2 domain). It starts finite so that
         // a masked key (score -inf) gives p = 0 rather than NaN.
         m_run[qb] = -1e30f;
@@ -281,10 +391,10 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
 
     if (ntiles > 0) {
         int koff[LPT], voff[LPT];
-        tile_offsets<C, PAD>(koff, voff, D, wave, lane);
+        tile_offsets<C, PAD>(koff, voff, D, (int)a.sk.s, (int)a.sv.s, wave, lane);
         auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
-            issue_tile<C>(Kh, t * C::BN, Skv, D, dst, wave, koff);
-            issue_tile<C>(Vh, t * C::BN, Skv, D, dst + TILE, wave, voff);
+            issue_tile<C>(Kh, t * C::BN, Skv, D, a.sk.s, dst, wave, koff);
+            issue_tile<C>(Vh, t * C::BN, Skv, D, a.sv.s, dst + TILE, wave, voff);
         };
         int kaddr[8];
         {
@@ -298,36 +408,33 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
             const int vv = NU >= 16 ? (j16 >> 2) : (j16 >> 3);
             const int w = 2 * (G & 1) + ((j16 & 3) >> 1);
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
-                vaddr[b] = vrow * RB + (4 * (b ^ vv) + w) * 16 + 8 * (j16 & 1);
+            for (int ob = 0; ob < 4; ++ob)
+                vaddr[ob] = vrow * RB + (4 * (ob ^ vv) + w) * 16 + 8 * (j16 & 1);
         }
 
-        // S^T of 32-key block kb of the tile in stage st, both query blocks.
+        // S^T of 32-key block kb of the tile in stage st, every query block.
         auto qk = [&](const char* st, int kb, f32x16 (&S)[QB]) __attribute__((always_inline)) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) S[qb] = f32x16{};
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
-                const f16x8 a = lds_read16(st, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
+                const x8 kf = lds_read16<T>(st, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
-                    S[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][s], S[qb], 0, 0, 0);
+                for (int qb = 0; qb < QB; ++qb) S[qb] = E::mma32(kf, qf[qb][s], S[qb]);
             }
         };
         // O^T += V^T P^T for 32-key block kb of the tile in stage st.
-        auto pv = [&](const char* st, int kb, const f16x8 (&P)[QB][2]) __attribute__((always_inline)) {
+        auto pv = [&](const char* st, int kb, const x8 (&P)[QB][2]) __attribute__((always_inline)) {
             const char* sv = st + TILE;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                for (int b = 0; b < NOB; ++b) {
-                    const int off = (2 * kb + ks) * 16 * RB + (b & ~3) * 64;
-                    const f16x4 lo = lds_read_tr(sv, vaddr[b & 3] + off);
-                    const f16x4 hi = lds_read_tr(sv, vaddr[b & 3] + off + 8 * RB);
-                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                for (int ob = 0; ob < NOB; ++ob) {
+                    const int off = vaddr[ob & 3] + (2 * kb + ks) * 16 * RB + (ob & ~3) * 64;
+                    const x8 vf = lds_read_tr2<T>(sv, off, off + 8 * RB);
 #pragma unroll
                     for (int qb = 0; qb < QB; ++qb)
-                        oacc[qb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[qb][ks], oacc[qb][b], 0, 0, 0);
+                        oacc[qb][ob] = E::mma32(vf, P[qb][ks], oacc[qb][ob]);
                 }
         };
         // Scores of keys >= Skv (block keys key0..key0+31) to -inf. Taken
@@ -350,12 +457,12 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
         // is taken, O and l are rescaled and P is recomputed (a per-wave
         // branch, so it stays uniform). Any rescale of O comes after the PV
         // MFMAs issued before this call.
-        auto softmax = [&](f32x16 (&S)[QB], f16x8 (&P)[QB][2]) __attribute__((always_inline)) {
+        auto softmax = [&](f32x16 (&S)[QB], x8 (&P)[QB][2]) __attribute__((always_inline)) {
             float lp[QB];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 lp[qb] = 0.f;
-                block_exp_f16(S[qb], P[qb][0], P[qb][1], -m_run[qb], c, lp[qb]);
+                block_exp<T>(S[qb], P[qb][0], P[qb][1], -m_run[qb], c, lp[qb]);
             }
             float lmax = lp[0];
 #pragma unroll
@@ -370,11 +477,11 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const float m_new = fmaxf(m_run[qb], mx);
                     const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
 #pragma unroll
-                    for (int b = 0; b < NOB; ++b) oacc[qb][b] *= alpha;
+                    for (int ob = 0; ob < NOB; ++ob) oacc[qb][ob] *= alpha;
                     l_run[qb] *= alpha;
                     m_run[qb] = m_new;
                     lp[qb] = 0.f;
-                    block_exp_f16(S[qb], P[qb][0], P[qb][1], -m_new, c, lp[qb]);
+                    block_exp<T>(S[qb], P[qb][0], P[qb][1], -m_new, c, lp[qb]);
                 }
             }
 #pragma unroll
@@ -382,11 +489,11 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
         };
 
         f32x16 Sa[QB], Sb[QB];
-        f16x8 Pa[QB][2], Pb[QB][2];
+        x8 Pa[QB][2], Pb[QB][2];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) Pb[qb][ks] = f16x8{};  // block -1: no keys
+            for (int ks = 0; ks < 2; ++ks) Pb[qb][ks] = x8{};  // block -1: no keys
 
         // Tile w (blocks 2w, 2w+1) in stage cur; prev holds tile w-1, nxt
         // tile w+1; fill (the stage of tile w-1) takes tile w+3.
@@ -440,19 +547,19 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
         const float l = half_swap_sum(l_run[qb]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         if (row < Sq) {
-            f16* op = Oh + (long)row * D;
+            T* op = Oh + row * a.so.s;
 #pragma unroll
-            for (int b = 0; b < NOB; ++b)
+            for (int ob = 0; ob < NOB; ++ob)
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const int d0 = 32 * b + 8 * rr + 4 * g;
+                    const int d0 = 32 * ob + 8 * rr + 4 * g;
                     if (!PAD || d0 < D) {
-                        const f16x2 h0 = __builtin_convertvector(
-                            f32x2{oacc[qb][b][4 * rr + 0] * inv, oacc[qb][b][4 * rr + 1] * inv}, f16x2);
-                        const f16x2 h1 = __builtin_convertvector(
-                            f32x2{oacc[qb][b][4 * rr + 2] * inv, oacc[qb][b][4 * rr + 3] * inv}, f16x2);
-                        const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
-                        *reinterpret_cast<f16x4*>(op + d0) = h;
+                        const auto h0 = E::cvt2(oacc[qb][ob][4 * rr + 0] * inv,
+                                                oacc[qb][ob][4 * rr + 1] * inv);
+                        const auto h1 = E::cvt2(oacc[qb][ob][4 * rr + 2] * inv,
+                                                oacc[qb][ob][4 * rr + 3] * inv);
+                        *reinterpret_cast<typename E::x4*>(op + d0) =
+                            typename E::x4{h0[0], h0[1], h1[0], h1[1]};
                     }
                 }
         }
@@ -465,14 +572,11 @@ attn_fwd_pipe(const f16* __restrict__ Q, const f16* __restrict__ K,
 //
 // With 32 query rows a wave would need a 256-register O accumulator; with 16
 // rows O^T is 32 blocks of 16x16 (128 registers) and two waves fit per SIMD.
-// Lane l = 16*g + i holds query i of the wave: the S^T = K Q^T accumulator of
-// a 16-key block gives it keys 4g..4g+3, so row reductions combine the four
-// lanes i, i+16, i+32, i+48. A 32-key tile is two score blocks feeding one
-// 16x16x32 PV step, whose B operand takes keys 4g..4g+3 of block 0 and of
-// block 1; V^T is read with ds_read_b64_tr_b16 in that key order.
+// A lane holds 4 keys of each 16-key score block (16x16 accumulator layout:
+// rows 4(l/16)..+3, column l%16), so row reductions combine four lanes.
 struct Cfg512 {
     static constexpr int DP = 512, NW = 8, BN = 32, BM = NW * 16, NT = NW * 64;
-    static constexpr int RB = DP * 2;  // bytes of one K or V row in HBM
+    static constexpr int RB = DP * 2;  // bytes of one K or V row
     // LDS rows are padded instead of swizzled (one direct-load instruction
     // fills exactly one row, so the padding costs nothing): with a 1040-byte
     // K stride the QK^T read (16 rows, one 16-byte unit each) and with a
@@ -485,40 +589,22 @@ struct Cfg512 {
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
-// Sum / max over lanes i, i+16, i+32, i+48.
-__device__ __forceinline__ float quad_group_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-__device__ __forceinline__ float quad_group_max(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-#endif
-
-#if defined(__HIP_DEVICE_COMPILE__)
 // Rare path of the D = 512 kernel: the tile's scores exceed the running max by
 // more than kTau. Returns the new max, the rescale factor for O and l, and P
 // and the tile's row sum recomputed with the new max. Kept out of line (and
 // away from O, which stays in registers) so the hot loop does not reserve
 // registers for it.
+template <class T>
 struct Rescale512 {
-    f16x8 P;
+    typename Elem<T>::x8 P;
     float m, alpha, l_tile;
 };
-__device__ __attribute__((noinline)) Rescale512 d512_rescale(f32x4 S0, f32x4 S1, float m_run,
-                                                             float c) {
+template <class T>
+__device__ __attribute__((noinline)) Rescale512<T> d512_rescale(f32x4 S0, f32x4 S1, float m_run,
+                                                                float c) {
     float mx = fmaxf(max3(S0[0], S0[1], S0[2]), max3(S0[3], S1[0], S1[1]));
     mx = quad_group_max(max3(mx, S1[2], S1[3])) * c;
-    Rescale512 r;
+    Rescale512<T> r;
     r.m = fmaxf(m_run, mx);
     r.alpha = __builtin_amdgcn_exp2f(m_run - r.m);
     const float nm = -r.m;
@@ -528,10 +614,10 @@ __device__ __attribute__((noinline)) Rescale512 d512_rescale(f32x4 S0, f32x4 S1,
         const f32x4& Sb = u < 2 ? S0 : S1;
         const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1)], c, nm));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1) + 1], c, nm));
-        const f16x2 hp = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+        const auto hp = Elem<T>::cvt2(p0, p1);
         r.P[2 * u] = hp[0];
         r.P[2 * u + 1] = hp[1];
-        lsum = __builtin_amdgcn_fdot2(hp, f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+        lsum = Elem<T>::sum2(hp, lsum);
     }
     r.l_tile = lsum;
     return r;
@@ -539,28 +625,33 @@ __device__ __attribute__((noinline)) Rescale512 d512_rescale(f32x4 S0, f32x4 S1,
 #endif
 
 // grid: ceil(Sq / 128) * B*H workgroups; block: 512 threads.
+template <class T>
 __global__ void __launch_bounds__(Cfg512::NT, 1)
-attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
-              const f16* __restrict__ V, f16* __restrict__ O,
-              int Sq, int Skv, float c, float qsign) {
+attn_fwd_d512(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
     using C = Cfg512;
-    constexpr int D = C::DP, BN = C::BN, RB = C::RB, NLD = C::NLD;
+    using E = Elem<T>;
+    using x8 = typename E::x8;
+    constexpr int D = C::DP, BN = C::BN, NLD = C::NLD;
     static_assert(NLD * C::NW == BN && D * 2 == 64 * 16, "one row per load instruction");
     constexpr int NQF = D / 32;  // Q fragments (32 dims each)
     constexpr int NOB = D / 16;  // 16-dim output blocks
     __shared__ __attribute__((aligned(1024))) char lds[C::LDS];  // 2 stages x (K, V)
 
+    const int Sq = a.Sq, Skv = a.Skv;
+    const float c = a.c;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    const long bh = blockIdx.x / nqt;
+    const int bh = blockIdx.x / nqt;
     const int qt = blockIdx.x % nqt;
-    const f16* Qh = Q + bh * (long)Sq * D;
-    const f16* Kh = K + bh * (long)Skv * D;
-    const f16* Vh = V + bh * (long)Skv * D;
-    f16* Oh = O + bh * (long)Sq * D;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+    T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
+    const long long kss = a.sk.s, vss = a.sv.s;
     const int qrow = qt * C::BM + wave * 16 + i;
     const bool live = qrow < Sq;
 
@@ -569,32 +660,31 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
     // 8l..8l+7. Rows past Skv read as zeros (the descriptor covers the valid
     // rows only).
     auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
-        const int bytes = min(Skv - t * BN, BN) * RB;
+        const int rows = min(Skv - t * BN, BN);
+        const int kbytes = (int)(((rows - 1) * kss + D) * 2);
+        const int vbytes = (int)(((rows - 1) * vss + D) * 2);
         const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + (long)t * BN * D), 0, bytes, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc((void*)(Kh + t * BN * kss), 0, kbytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + (long)t * BN * D), 0, bytes, 0x00020000);
+            __builtin_amdgcn_make_buffer_rsrc((void*)(Vh + t * BN * vss), 0, vbytes, 0x00020000);
 #pragma unroll
         for (int n = 0; n < NLD; ++n) {
             const int row = wave + n * C::NW;  // wave-uniform
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + row * C::KS), 16,
-                                                     lane * 16, row * RB, 0, 0);
+                                                     lane * 16, (int)(row * kss * 2), 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(dst + C::KTILE + row * C::VS),
-                                                     16, lane * 16, row * RB, 0, 0);
+                                                     16, lane * 16, (int)(row * vss * 2), 0, 0);
         }
     };
     const int ntiles = (Skv + BN - 1) / BN;
     if (ntiles > 0) issue(0, stage(0));
 
     // Q^T fragments (B operand: column = this lane's query, k = dims 32s+8g..).
-    f16x8 qf[NQF];
-    const unsigned qneg = qsign < 0.f ? 0x80008000u : 0u;
+    x8 qf[NQF];
+    const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int s = 0; s < NQF; ++s) {
-        f16x8 val = {};
-        if (live) val = ld_global16(Qh + (long)qrow * D + 32 * s + 8 * g);
-        qf[s] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, val) ^ qneg);
-    }
+    for (int s = 0; s < NQF; ++s)
+        qf[s] = q_fragment(Qh + qrow * a.sq.s + 32 * s + 8 * g, live, qneg);
 
     // K read: row kb*16 + i, dims 32s + 8g.. ; V^T read (transposed, per
     // 16-lane group g): row 4g + i/4 (+16 for the second key half), dims
@@ -604,27 +694,25 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
 
     f32x4 oacc[NOB];
 #pragma unroll
-    for (int b = 0; b < NOB; ++b) oacc[b] = f32x4{};
-    float m_run = -1e30f;  // running max (log2 units); finite, see attn_fwd_mfma
+    for (int ob = 0; ob < NOB; ++ob) oacc[ob] = f32x4{};
+    float m_run = -1e30f;  // running max (log2 units); finite so masked keys give p = 0
     float l_run = 0.f;
 
-    // P (B operand of the PV step) from the two score blocks, with running max -nm.
-    auto make_p = [&](const f32x4 (&S)[2], f16x8& P, float nm, float& lsum, f16x2& pm)
+    // P (B operand of the PV step) from the two score blocks, with running
+    // max -nm; pm tracks the largest p.
+    auto make_p = [&](const f32x4 (&S)[2], x8& P, float nm, float& lsum, f32x2& pm)
         __attribute__((always_inline)) {
-        f16x2 hp[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const f32x4& Sb = S[u >> 1];
             const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1)], c, nm));
             const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1) + 1], c, nm));
-            hp[u] = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-            P[2 * u] = hp[u][0];
-            P[2 * u + 1] = hp[u][1];
-            lsum = __builtin_amdgcn_fdot2(hp[u], f16x2{(f16)1.0f, (f16)1.0f}, lsum, false);
+            const auto hp = E::cvt2(p0, p1);
+            P[2 * u] = hp[0];
+            P[2 * u + 1] = hp[1];
+            lsum = E::sum2(hp, lsum);
+            pm[u & 1] = max3(pm[u & 1], p0, p1);
         }
-        pm = __builtin_elementwise_maximum(pm, __builtin_elementwise_maximum(
-                                                   __builtin_elementwise_maximum(hp[0], hp[1]),
-                                                   __builtin_elementwise_maximum(hp[2], hp[3])));
     };
 
     auto tile = [&](int t, char* __restrict__ nxt, const char* __restrict__ cur)
@@ -638,8 +726,8 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
             f32x4 Sp[2] = {f32x4{}, f32x4{}};
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
-                const f16x8 a = lds_read16(sk, kbase + kb * 16 * C::KS + s * 64);
-                Sp[s & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s], Sp[s & 1], 0, 0, 0);
+                const x8 kf = lds_read16<T>(sk, kbase + kb * 16 * C::KS + s * 64);
+                Sp[s & 1] = E::mma16(kf, qf[s], Sp[s & 1]);
             }
             __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
 #pragma unroll
@@ -661,18 +749,18 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
             float mx = fmaxf(max3(S[0][0], S[0][1], S[0][2]), max3(S[0][3], S[1][0], S[1][1]));
             m_run = quad_group_max(max3(mx, S[1][2], S[1][3])) * c;
         }
-        f16x8 P;
+        x8 P;
         float l_tile = 0.f;
-        f16x2 pm = {(f16)0.0f, (f16)0.0f};
+        f32x2 pm = {0.f, 0.f};
         make_p(S, P, -m_run, l_tile, pm);
-        const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+        const float pmax = fmaxf(pm[0], pm[1]);
         // The O rescale runs on every tile (alpha = 1.0 exactly unless the rare
         // path ran): a conditional in-place rescale of the 128-register
         // accumulator costs more registers than two waves per SIMD allow, while
         // 128 multiplies per tile hide under its 64 MFMAs.
         float alpha = 1.f;
-        if (__builtin_expect(__any(pmax > kPmaxLimit), 0)) {
-            const Rescale512 r = d512_rescale(S[0], S[1], m_run, c);
+        if (__builtin_expect(__any(!(pmax <= kPmaxLimit)), 0)) {
+            const Rescale512<T> r = d512_rescale<T>(S[0], S[1], m_run, c);
             alpha = r.alpha;
             l_run *= r.alpha;
             m_run = r.m;
@@ -680,15 +768,13 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
             l_tile = r.l_tile;
         }
 #pragma unroll
-        for (int b = 0; b < NOB; ++b) oacc[b] *= alpha;
+        for (int ob = 0; ob < NOB; ++ob) oacc[ob] *= alpha;
         l_run += l_tile;
         // O^T += V^T P^T, one 16x16x32 MFMA per 16-dim block.
 #pragma unroll
-        for (int b = 0; b < NOB; ++b) {
-            const f16x4 lo = lds_read_tr(sv, vbase + 32 * b);
-            const f16x4 hi = lds_read_tr(sv, vbase + 32 * b + 16 * C::VS);
-            const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            oacc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P, oacc[b], 0, 0, 0);
+        for (int ob = 0; ob < NOB; ++ob) {
+            const x8 vf = lds_read_tr2<T>(sv, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
+            oacc[ob] = E::mma16(vf, P, oacc[ob]);
         }
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
 #pragma unroll
@@ -708,20 +794,18 @@ attn_fwd_d512(const f16* __restrict__ Q, const f16* __restrict__ K,
     const float l = quad_group_sum(l_run);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (live) {
-        f16* op = Oh + (long)qrow * D + 4 * g;
+        T* op = Oh + qrow * a.so.s + 4 * g;
 #pragma unroll
-        for (int b = 0; b < NOB; ++b) {
-            const f16x2 h0 = __builtin_convertvector(f32x2{oacc[b][0] * inv, oacc[b][1] * inv}, f16x2);
-            const f16x2 h1 = __builtin_convertvector(f32x2{oacc[b][2] * inv, oacc[b][3] * inv}, f16x2);
-            const f16x4 h = {h0[0], h0[1], h1[0], h1[1]};
-            *reinterpret_cast<f16x4*>(op + 16 * b) = h;
+        for (int ob = 0; ob < NOB; ++ob) {
+            const auto h0 = E::cvt2(oacc[ob][0] * inv, oacc[ob][1] * inv);
+            const auto h1 = E::cvt2(oacc[ob][2] * inv, oacc[ob][3] * inv);
+            *reinterpret_cast<typename E::x4*>(op + 16 * ob) =
+                typename E::x4{h0[0], h0[1], h1[0], h1[1]};
         }
     }
 #endif
 }
 
-// Tile configurations per head-dim class (waves per workgroup, keys per
-// tile, waves per SIMD); the macros exist for tuning sweeps.
 thread_local char g_err[256];
 
 void set_err(const char* msg) {
@@ -733,38 +817,65 @@ void set_err(const char* msg) {
 using Cfg128 = Cfg<128, 8, 1, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
 using Cfg64 = Cfg<64, 8, 1, 2>;    // 64 KB: two workgroups, four waves per SIMD
 
-template <class C, bool PAD>
-hipError_t launch_pipe(const void* q, const void* k, const void* v, void* o, int B, int H,
-                      int Sq, int Skv, int D, float scale, hipStream_t s) {
-    dim3 grid((unsigned)((Sq + C::BM - 1) / C::BM) * (unsigned)(B * H));
-    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);  // see launch_cfg
-    const float qsign = scale < 0.f ? -1.f : 1.f;
-    hipLaunchKernelGGL((attn_fwd_pipe<C, PAD>), grid, dim3(C::NT), 0, s, (const f16*)q,
-                       (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, D, c, qsign);
+template <class T>
+hipError_t launch_t(const KArgs& a, int BH, hipStream_t s) {
+    const int D = a.D;
+    if (D == 512) {
+        dim3 grid((unsigned)((a.Sq + Cfg512::BM - 1) / Cfg512::BM) * (unsigned)BH);
+        hipLaunchKernelGGL((attn_fwd_d512<T>), grid, dim3(Cfg512::NT), 0, s, a);
+    } else if (D == 128) {
+        dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * (unsigned)BH);
+        hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T>), grid, dim3(Cfg128::NT), 0, s, a);
+    } else {
+        dim3 grid((unsigned)((a.Sq + Cfg64::BM - 1) / Cfg64::BM) * (unsigned)BH);
+        if (D == 64)
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T>), grid, dim3(Cfg64::NT), 0, s, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T>), grid, dim3(Cfg64::NT), 0, s, a);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_d512(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
-                       int Skv, float scale, hipStream_t s) {
-    dim3 grid((unsigned)((Sq + Cfg512::BM - 1) / Cfg512::BM) * (unsigned)(B * H));
-    const float c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);  // see launch_cfg
-    const float qsign = scale < 0.f ? -1.f : 1.f;
-    hipLaunchKernelGGL(attn_fwd_d512, grid, dim3(Cfg512::NT), 0, s, (const f16*)q,
-                       (const f16*)k, (const f16*)v, (f16*)o, Sq, Skv, c, qsign);
-    return hipGetLastError();
+// Whether the rows of an output tensor can overlap: the (stride, size)
+// pairs of its batch, head and sequence dims, sorted by stride, must each
+// step past everything the smaller ones span (innermost: D contiguous
+// elements). Dims of size 1 are ignored.
+bool output_overlaps(const Strides3& s, int B, int H, int Sq, int D) {
+    long long st[3] = {s.b, s.h, s.s};
+    long long n[3] = {B, H, Sq};
+    for (int i = 0; i < 3; ++i)
+        for (int j = i + 1; j < 3; ++j)
+            if (st[j] < st[i]) {
+                long long t = st[i];
+                st[i] = st[j];
+                st[j] = t;
+                t = n[i];
+                n[i] = n[j];
+                n[j] = t;
+            }
+    long long extent = D;
+    for (int i = 0; i < 3; ++i) {
+        if (n[i] <= 1) continue;
+        if (st[i] < extent) return true;
+        extent = st[i] * (n[i] - 1) + extent;
+    }
+    return false;
 }
 
-// Validates the arguments; returns 0 and the workspace size, or 1 with the
-// error message set.
 // Validates the arguments; returns 0, or 1 with the error message set.
 int check_args(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
-               int Skv, int D) {
+               int Skv, int D, int dtype, const Strides3& sq, const Strides3& sk,
+               const Strides3& sv, const Strides3& so) {
     if (B < 0 || H < 0 || Sq < 0 || Skv < 0) {
         set_err("attn: negative size");
         return 1;
     }
     if (!((D <= 64 && D > 0 && D % 8 == 0) || D == 128 || D == 512)) {
         set_err("attn: head_dim must be <=64 and a multiple of 8, or 128, or 512");
+        return 1;
+    }
+    if (dtype != ATTN_DTYPE_F16 && dtype != ATTN_DTYPE_BF16) {
+        set_err("attn: dtype must be ATTN_DTYPE_F16 or ATTN_DTYPE_BF16");
         return 1;
     }
     if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL || (long)B * H > 65535) {
@@ -776,20 +887,76 @@ int check_args(const void* q, const void* k, const void* v, void* o, int B, int 
         set_err("attn: null pointer");
         return 1;
     }
+    // 16-byte vector loads of q, k, v and 8-byte stores of o.
+    const Strides3* in[3] = {&sq, &sk, &sv};
+    for (const Strides3* s : in)
+        if (s->b < 0 || s->h < 0 || s->s < 0 || s->b % 8 || s->h % 8 || s->s % 8) {
+            set_err("attn: q/k/v strides must be non-negative multiples of 8 elements");
+            return 1;
+        }
+    if (so.b < 0 || so.h < 0 || so.s < 0 || so.b % 4 || so.h % 4 || so.s % 4) {
+        set_err("attn: o strides must be non-negative multiples of 4 elements");
+        return 1;
+    }
+    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 || (uintptr_t)o % 8) {
+        set_err("attn: q/k/v must be 16-byte and o 8-byte aligned");
+        return 1;
+    }
+    // K/V tile offsets and buffer ranges are 32-bit: 64 rows of the sequence
+    // stride must stay below 2^31 bytes.
+    if (sk.s > (1 << 24) || sv.s > (1 << 24)) {
+        set_err("attn: k/v sequence stride above 2^24 elements");
+        return 1;
+    }
+    if (output_overlaps(so, B, H, Sq, D)) {
+        set_err("attn: o strides make output rows overlap");
+        return 1;
+    }
     return 0;
 }
 
-int run(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq, int Skv,
-        int D, float scale, hipStream_t s) {
-    hipError_t e;
-    if (D == 128)
-        e = launch_pipe<Cfg128, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
-    else if (D == 64)
-        e = launch_pipe<Cfg64, false>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
-    else if (D == 512)
-        e = launch_d512(q, k, v, o, B, H, Sq, Skv, scale, s);
-    else
-        e = launch_pipe<Cfg64, true>(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+Strides3 contiguous(int H, int S, int D) {
+    return Strides3{(long long)H * S * D, (long long)S * D, D};
+}
+
+}  // namespace
+
+extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr; }
+
+extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o, int B, int H,
+                           int Sq, int Skv, int D, float scale, hipStream_t stream, int dtype,
+                           const long long* q_strides, const long long* k_strides,
+                           const long long* v_strides, const long long* o_strides) {
+    g_err[0] = 0;
+    auto pick = [](const long long* p, Strides3 dflt) {
+        return p ? Strides3{p[0], p[1], p[2]} : dflt;
+    };
+    const Strides3 sq = pick(q_strides, contiguous(H, Sq, D));
+    const Strides3 sk = pick(k_strides, contiguous(H, Skv, D));
+    const Strides3 sv = pick(v_strides, contiguous(H, Skv, D));
+    const Strides3 so = pick(o_strides, contiguous(H, Sq, D));
+    if (check_args(q, k, v, o, B, H, Sq, Skv, D, dtype, sq, sk, sv, so)) return 1;
+    if (B == 0 || H == 0 || Sq == 0) return 0;
+    KArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.sq = sq;
+    a.sk = sk;
+    a.sv = sv;
+    a.so = so;
+    a.H = H;
+    a.Sq = Sq;
+    a.Skv = Skv;
+    a.D = D;
+    // Masked keys carry score -inf and rely on c > 0 (-inf * 0 is NaN). For
+    // scale == 0, c = 1e-30 gives exp2(s*c - m) == 1.0f exactly for every
+    // finite score, i.e. the same uniform weights as c == 0.
+    a.c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
+    a.qsign = scale < 0.f ? -1.f : 1.f;
+    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, B * H, stream)
+                                                  : launch_t<f16>(a, B * H, stream);
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;
@@ -797,16 +964,10 @@ int run(const void* q, const void* k, const void* v, void* o, int B, int H, int 
     return 0;
 }
 
-}  // namespace
-
-extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr; }
-
 extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,
                         int Sq, int Skv, int D, float scale, hipStream_t s) {
-    g_err[0] = 0;
-    if (check_args(q, k, v, o, B, H, Sq, Skv, D)) return 1;
-    if (B == 0 || H == 0 || Sq == 0) return 0;
-    return run(q, k, v, o, B, H, Sq, Skv, D, scale, s);
+    return attn_fwd_ex(q, k, v, o, B, H, Sq, Skv, D, scale, s, ATTN_DTYPE_F16, nullptr, nullptr,
+                       nullptr, nullptr);
 }
 
 extern "C" void launch(const void* q, const void* k, const void* v, void* o, int B, int H,

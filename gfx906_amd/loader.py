@@ -64,6 +64,9 @@ def capi() -> ctypes.CDLL:
     lib.launch.restype = None
     lib.attn_fwd.argtypes = args
     lib.attn_fwd.restype = ctypes.c_int
+    strides = ctypes.POINTER(ctypes.c_longlong)
+    lib.attn_fwd_ex.argtypes = args + [ctypes.c_int] + [strides] * 4
+    lib.attn_fwd_ex.restype = ctypes.c_int
     lib.attn_last_error.argtypes = []
     lib.attn_last_error.restype = ctypes.c_char_p
     return lib

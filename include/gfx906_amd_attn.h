@@ -1,11 +1,13 @@
 /* C ABI of the MI355X (gfx950) flash-attention forward.
  *
- * All pointers are device pointers to contiguous fp16 tensors:
+ * All pointers are device pointers. For launch() and attn_fwd() the tensors
+ * are contiguous fp16:
  *   q, o : [B, H, Sq,  D]
  *   k, v : [B, H, Skv, D]
+ * attn_fwd_ex() also takes bf16 and per-tensor strides.
  * D must be <= 64 and a multiple of 8, or 128, or 512. Sq != Skv is allowed.
  * o[b,h,i,:] = sum_j softmax_j(scale * <q[b,h,i,:], k[b,h,j,:]>) v[b,h,j,:],
- * rounded to fp16; rows with Skv == 0 are written as zeros.
+ * rounded to the element type; rows with Skv == 0 are written as zeros.
  * Calls are asynchronous on `stream` and keep no state between calls.
  */
 #ifndef GFX906_AMD_ATTN_H
@@ -16,6 +18,10 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Element types for attn_fwd_ex(). */
+#define ATTN_DTYPE_F16 0
+#define ATTN_DTYPE_BF16 1
 
 /* Drop-in for the reference entry point of the same name and signature:
  * declared at attn.cpp:4-5, defined at attn_kernel.hip:710-742. Returns
@@ -31,9 +37,25 @@ void launch(const void* q, const void* k, const void* v, void* o,
 int attn_fwd(const void* q, const void* k, const void* v, void* o,
              int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream);
 
-/* Message for the last failed launch()/attn_fwd() on the calling thread, or
- * NULL if the last call succeeded. No counterpart in the reference, whose
- * launch() (attn_kernel.hip:710-742) never reports errors. */
+/* attn_fwd() for fp16 or bf16 (dtype = ATTN_DTYPE_F16 / ATTN_DTYPE_BF16,
+ * the same type for q, k, v and o) and strided tensors. Each *_strides
+ * points to three element strides {batch, head, sequence} of that tensor,
+ * or is NULL for the contiguous layout; the head dim is always contiguous.
+ * q, k, v need 16-byte alignment and strides that are multiples of 8
+ * elements, o 8-byte alignment and multiples of 4; k/v sequence strides
+ * are at most 2^24; input strides may be 0 (a tensor broadcast over batch or
+ * heads) but output rows must not overlap. Return codes as attn_fwd().
+ * No counterpart in the reference, whose hook casts bf16 to fp16 and back
+ * (deploy/gfx906_attention.py:71-75, 99-100) and whose binding copies
+ * strided inputs (attn.cpp:15). */
+int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
+                int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream,
+                int dtype, const long long* q_strides, const long long* k_strides,
+                const long long* v_strides, const long long* o_strides);
+
+/* Message for the last failed launch()/attn_fwd()/attn_fwd_ex() on the
+ * calling thread, or NULL if the last call succeeded. No counterpart in the
+ * reference, whose launch() (attn_kernel.hip:710-742) never reports errors. */
 const char* attn_last_error(void);
 
 #ifdef __cplusplus

@@ -97,3 +97,61 @@ def test_product_package_never_imports_oracle():
 def test_flops_formula():
     # flops_probe.py:18: 4*B*H*S*S*D
     assert gfx906_amd.flops(1, 16, 16384, 16384, 128) == 2_199_023_255_552
+
+
+# -- attn_fwd_ex: rejected before any HIP call ---------------------------------------------
+
+P = ctypes.c_void_p(0x10000)  # aligned, never dereferenced: every case below is rejected
+
+
+def _ex(B=1, H=2, Sq=16, Skv=16, D=64, dtype=0, q=None, k=None, v=None, o=None, ptrs=None):
+    lib = gfx906_amd.capi()
+    arr = [None if s is None else (ctypes.c_longlong * 3)(*s) for s in (q, k, v, o)]
+    pq, pk, pv, po = ptrs or (P, P, P, P)
+    rc = lib.attn_fwd_ex(pq, pk, pv, po, B, H, Sq, Skv, D, 0.1, None, dtype, *arr)
+    return rc, lib.attn_last_error()
+
+
+def test_ex_rejects_unknown_dtype():
+    assert _ex(dtype=2) == (1, b"attn: dtype must be ATTN_DTYPE_F16 or ATTN_DTYPE_BF16")
+
+
+@pytest.mark.parametrize("which", ["q", "k", "v"])
+def test_ex_rejects_input_strides_not_multiple_of_8(which):
+    rc, err = _ex(**{which: (2 * 16 * 64, 16 * 64, 60)})
+    assert rc == 1 and b"multiples of 8" in err
+    rc, err = _ex(**{which: (-8, 16 * 64, 64)})
+    assert rc == 1 and b"non-negative" in err
+
+
+def test_ex_rejects_output_strides_and_overlap():
+    assert _ex(o=(2 * 16 * 64, 16 * 64, 62))[1].startswith(b"attn: o strides must")
+    # all query rows of a head written to one row
+    assert b"overlap" in _ex(o=(2 * 64, 64, 0))[1]
+    # heads interleaved onto each other: head stride smaller than a row
+    assert b"overlap" in _ex(o=(2 * 16 * 64, 32, 64 * 2))[1]
+
+
+def test_ex_rejects_misaligned_pointers():
+    rc, err = _ex(ptrs=(ctypes.c_void_p(0x10008), P, P, P))
+    assert rc == 1 and b"aligned" in err
+    rc, err = _ex(ptrs=(P, P, P, ctypes.c_void_p(0x10004)))
+    assert rc == 1 and b"aligned" in err
+
+
+def test_ex_rejects_huge_kv_sequence_stride():
+    rc, err = _ex(k=(0, 0, (1 << 24) + 8))
+    assert rc == 1 and b"2^24" in err
+
+
+def test_ex_null_strides_mean_contiguous_and_empty_is_no_op():
+    lib = gfx906_amd.capi()
+    assert lib.attn_fwd_ex(None, None, None, None, 0, 2, 16, 16, 64, 0.1, None, 1,
+                           None, None, None, None) == 0
+    assert lib.attn_last_error() is None
+
+
+def test_header_dtype_codes():
+    text = open(HEADER).read()
+    assert re.search(r"#define ATTN_DTYPE_F16 0\b", text)
+    assert re.search(r"#define ATTN_DTYPE_BF16 1\b", text)

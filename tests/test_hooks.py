@@ -115,14 +115,19 @@ def test_container_requires_skip_reshape():
 
 
 def test_container_kernel_path_layout_and_bf16():
-    """Kernel path with the op replaced by SDPA on CPU: checks the bf16 cast and
-    the [B, H, S, D] -> [B, S, H*D] output reshape."""
-    seen = {}
+    """Kernel path with the op replaced by SDPA on CPU: bf16 reaches the op
+    uncast, and the [B, S, H*D] result is the op's output written through an
+    ``out`` view of a [B, S, H, D] buffer (no transpose copy afterwards)."""
+    seen = []
 
-    def fake_attn(q, k, v, scale):
-        seen["dtype"], seen["scale"] = q.dtype, scale
-        return torch.nn.functional.scaled_dot_product_attention(
-            q.float(), k.float(), v.float(), scale=scale).half()
+    def fake_attn(q, k, v, scale, out=None):
+        seen.append((q.dtype, scale, out))
+        res = torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float(), v.float(), scale=scale).to(q.dtype)
+        if out is None:
+            return res
+        out.copy_(res)
+        return out
 
     mod = types.SimpleNamespace(attn=fake_attn)
     g = torch.Generator().manual_seed(0)
@@ -132,8 +137,10 @@ def test_container_kernel_path_layout_and_bf16():
         out = hooks.container_attn(Box(q), Box(k), Box(v), 3, skip_reshape=True)
         out_bhsd = hooks.container_attn(Box(q), Box(k), Box(v), 3, skip_reshape=True,
                                          skip_output_reshape=True, scale=0.3)
-    assert seen["dtype"] == torch.float16 and seen["scale"] == 0.3
-    assert out.dtype == torch.bfloat16 and out.shape == (2, 5, 3 * 16)
+    (dt0, sc0, view), (dt1, sc1, none) = seen
+    assert dt0 == dt1 == torch.bfloat16 and sc0 == 16 ** -0.5 and sc1 == 0.3 and none is None
+    assert view.shape == (2, 3, 5, 16) and view.data_ptr() == out.data_ptr()
+    assert out.dtype == torch.bfloat16 and out.shape == (2, 5, 3 * 16) and out.is_contiguous()
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
     torch.testing.assert_close(out.float(), ref.transpose(1, 2).reshape(2, 5, 48), atol=2e-2,
                                rtol=0)
