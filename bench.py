@@ -42,9 +42,13 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--workload", default="ns", choices=["ns", "c1", "c2", "c3", "c4", "c5"],
+    ap.add_argument("--workload", default="ns",
+                    choices=["ns", "c1", "c2", "c3", "c4", "c5", "conv3d_vae"],
                     help="BASELINE.json config to run (default: the north star the metric is "
-                         "quoted on; others are for profiling)")
+                         "quoted on; others are for profiling; conv3d_vae times the conv3d "
+                         "kernel on a 512->512 3x3x3 VAE layer)")
+    ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
+                    help="attention input type (profiling; the metric is quoted for fp16)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="instead of attention, time a plain device copy of this many bytes "
                          "(reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -88,6 +92,61 @@ def read_profile_figures():
     return out
 
 
+def conv3d_bench(args):
+    """conv3d kernel on a VAE decoder layer: x [1, 512, 8, 64, 64] NDHWC fp16,
+    w [512, 512, 3, 3, 3], bias; one JSON line (profiling, not the metric)."""
+    import torch
+
+    import gfx906_amd
+    from gfx906_amd import kitchen
+
+    g = torch.Generator().manual_seed(7)
+    n, c, d, h, wd, k, t = 1, 512, 8, 64, 64, 512, 3
+    cl = torch.channels_last_3d
+    x = (torch.randn(n, c, d, h, wd, generator=g) * 0.25).half().cuda().contiguous(memory_format=cl)
+    w = (torch.randn(k, c, t, t, t, generator=g) * 0.25).half().cuda().contiguous(memory_format=cl)
+    b = torch.randn(k, generator=g).half().cuda()
+    z, p, q = d - t + 1, h - t + 1, wd - t + 1
+    out = torch.empty(n, k, z, p, q, dtype=torch.float16, device="cuda").contiguous(
+        memory_format=cl)
+    dims = [n, d, h, wd, c, k, t, t, t, 1, 1, 1, z, p, q]
+    xs, os_ = list(kitchen._packed_strides(x.shape)), list(kitchen._packed_strides(out.shape))
+    conv = gfx906_amd.extension().conv3d
+
+    def call():
+        conv(x, w, b, None, out, dims, xs, os_, [0, 0, 0, 0])
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        call()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = [s_.elapsed_time(e_) for s_, e_ in zip(starts, ends)]
+    avg = sum(kernel_ms) / len(kernel_ms)
+    flops = 2 * n * z * p * q * k * c * t ** 3
+    achieved = flops / (avg * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "conv3d fwd TFLOP/s (fp16 NDHWC implicit GEMM), 1xMI355X",
+        "value": round(flops * args.steps / wall / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
+        "dtype": "fp16", "data": "synthetic: x, w ~ 0.25 N(0,1), bias ~ N(0,1), seeded",
+        "config": {"workload": "conv3d x[1,512,8,64,64] w[512,512,3,3,3] stride 1, bias"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "kernel_ms_avg": round(avg, 4), "kernel_ms_min": round(min(kernel_ms), 4),
+                     "algorithmic_flops_per_launch": flops},
+        "cpu_baseline": None}), flush=True)
+
+
 def cpu_baseline():
     """torch SDPA MATH on CPU, fp32 upcast, 2 heads of the workload (min of 3)."""
     import torch
@@ -128,18 +187,21 @@ def main():
         copy_calibration(args.copy_bytes, args.steps)
         return
 
-    import gfx906_amd
-    from oracle.attention import make_inputs
+    if args.workload == "conv3d_vae":
+        conv3d_bench(args)
+        return
 
-    from oracle.attention import CONFIGS
+    import gfx906_amd
+    from oracle.attention import CONFIGS, make_inputs
 
     if args.workload == "ns":
         w, mults, seed = WORKLOAD, (1.0, 1.0), SEED
     else:
         B, H, Sq, Skv, D, qm, vm, seed = CONFIGS[args.workload]
         w, mults = dict(B=B, H=H, Sq=Sq, Skv=Skv, D=D), (qm, vm)
-    q, k, v = (t.to("cuda") for t in make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"],
-                                                  *mults, seed=seed))
+    dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    q, k, v = (t.to("cuda", dt) for t in make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"],
+                                                      *mults, seed=seed))
     scale = w["D"] ** -0.5
     attn = gfx906_amd.extension().attn
     flops = gfx906_amd.flops(w["B"], w["H"], w["Sq"], w["Skv"], w["D"])
@@ -178,10 +240,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: q,k,v ~ N(0,1) fp16 from a seeded CPU generator",
+        "dtype": args.dtype,
+        "data": f"synthetic: q,k,v ~ N(0,1) {args.dtype} from a seeded CPU generator",
         "config": {"workload": (f"attn_fwd B{w['B']} H{w['H']} Sq{w['Sq']} Skv{w['Skv']} "
-                                f"D{w['D']} fp16, scale 1/sqrt(D), no mask ("
+                                f"D{w['D']} {args.dtype}, scale 1/sqrt(D), no mask ("
                                 + ("BASELINE.json north star" if args.workload == "ns"
                                    else f"BASELINE.json config {args.workload}") + ")"), **w,
                    "parallelism": "single GPU"},
@@ -204,7 +266,7 @@ def main():
                      "source": os.path.relpath(TRAFFIC_FILE, ROOT)
                      if os.path.isfile(TRAFFIC_FILE) else None},
     }
-    if not args.no_cpu and args.workload == "ns":
+    if not args.no_cpu and args.workload == "ns" and args.dtype == "fp16":
         result["cpu_baseline"] = cpu_baseline()
     else:
         result["cpu_baseline"] = None

@@ -2,12 +2,14 @@
 
 Two shared objects are produced under ``gfx906_amd/lib/``:
 
-* ``libgfx906_amd_attn.so`` -- the HIP kernels and the C ABI declared in
-  ``include/gfx906_amd_attn.h``, compiled by ``hipcc --offload-arch=gfx950``.
-  This plays the part of the reference's separately compiled
-  ``attn_kernel.o`` (README.md:12, deploy/gfx906_attn.py:40-59).
-* ``gfx906_amd_attn_ext.so`` -- the PyTorch binding ``attn(q, k, v, scale)``
-  (counterpart of the reference's attn.cpp built by
+* ``libgfx906_amd_attn.so`` -- the HIP kernels and the C ABIs declared in
+  ``include/gfx906_amd_attn.h`` and ``include/gfx906_amd_conv3d.h``, compiled
+  by ``hipcc --offload-arch=gfx950``. This plays the part of the reference's
+  separately compiled ``attn_kernel.o`` and ``conv3d_kernel.<arch>.o``
+  (README.md:12, deploy/gfx906_attn.py:40-59, gfx906_kitchen.py:58-76).
+* ``gfx906_amd_attn_ext.so`` -- the PyTorch bindings ``attn(q, k, v, scale)``
+  and ``conv3d(x, w, bias, res, out, dims, xs, os, rs)`` (counterparts of
+  the reference's attn.cpp and hip_conv/conv3d.cpp built by
   ``cpp_extension.load``, README.md:13), linked against the library above
   with an ``$ORIGIN`` rpath so the pair loads from the package directory.
 
@@ -51,18 +53,22 @@ def _run(cmd, cwd=None):
     return res
 
 
+KERNEL_SOURCES = ["attn_kernel.hip", "conv3d_kernel.hip"]
+BINDING_SOURCES = ["attn.cpp", "conv3d.cpp", "module.cpp"]
+
+
 def build_kernel_lib(extra_flags=()) -> Path:
-    """Compile csrc/attn_kernel.hip into the C-ABI shared library."""
+    """Compile the HIP sources into the C-ABI shared library."""
     LIB.mkdir(exist_ok=True)
     tmp = KERNEL_LIB.with_suffix(".so.tmp")
     _run([hipcc(), *HIP_FLAGS, *extra_flags, "-shared", f"-I{ROOT / 'include'}",
-          str(CSRC / "attn_kernel.hip"), "-o", str(tmp)])
+          *[str(CSRC / f) for f in KERNEL_SOURCES], "-o", str(tmp)])
     os.replace(tmp, KERNEL_LIB)
     return KERNEL_LIB
 
 
 def build_extension() -> Path:
-    """Compile csrc/attn.cpp into the torch extension, linked to the kernel lib.
+    """Compile the binding sources into the torch extension, linked to the kernel lib.
 
     The binding is plain C++ (no device code), so it is compiled by the host
     compiler with torch's include and library paths; no source translation
@@ -85,7 +91,7 @@ def build_extension() -> Path:
            f"-DTORCH_EXTENSION_NAME={EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
            *[f"-I{i}" for i in incs],
-           str(CSRC / "attn.cpp"), "-o", str(tmp),
+           *[str(CSRC / f) for f in BINDING_SOURCES], "-o", str(tmp),
            f"-L{LIB}", "-lgfx906_amd_attn",
            *[f"-L{d}" for d in libdirs],
            "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-ltorch_python",

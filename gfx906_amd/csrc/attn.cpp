@@ -27,6 +27,7 @@
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
 
+#include "bindings.h"
 #include "gfx906_amd_attn.h"
 
 namespace {
@@ -99,8 +100,3 @@ torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double sca
     return o;
 }
 
-PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.def("attn", &attn, "fp16/bf16 attention forward on gfx950 (q, k, v, scale, out=None)",
-          pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("scale"),
-          pybind11::arg("out") = pybind11::none());
-}

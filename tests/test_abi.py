@@ -16,17 +16,23 @@ from gfx906_amd import loader
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "gfx906_amd_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
-def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)
+def declared_functions(headers=None):
+    names = []
+    for h in headers or HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names += re.findall(r"^\s*[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)
+    return names
 
 
-def test_header_declares_reference_entry_point():
+def test_header_declares_reference_entry_points():
     names = declared_functions()
     assert "launch" in names and "attn_fwd" in names and "attn_last_error" in names
+    assert {"launch_conv3d", "conv3d_fwd", "conv3d_last_error"} <= set(names)
+    assert len(HEADERS) == 2
 
 
 def test_library_exports_every_declared_symbol():
@@ -155,3 +161,49 @@ def test_header_dtype_codes():
     text = open(HEADER).read()
     assert re.search(r"#define ATTN_DTYPE_F16 0\b", text)
     assert re.search(r"#define ATTN_DTYPE_BF16 1\b", text)
+
+
+def test_launch_conv3d_signature_matches_reference():
+    # hip_conv/conv3d_kernel.hip:218-225 (stream: hipStream_t, void* in the binding's copy)
+    text = re.sub(r"\s+", " ", open(os.path.join(ROOT, "include", "gfx906_amd_conv3d.h")).read())
+    assert ("void launch_conv3d(const void* x, const void* w, const void* bias, const void* res, "
+            "void* out, int nB, int D, int H, int W, int C, int K, int T, int R, int S, int sd, "
+            "int sh, int sw, int Z, int P, int Q, long M, long xsn, long xsd, long xsh, long xsw, "
+            "long osn, long osz, long osp, long osq, long rsn, long rsz, long rsp, long rsq, "
+            "hipStream_t stream);") in text
+
+
+def _conv(**kw):
+    """conv3d_fwd with a valid 1x8x4x6x6 -> 8x3x3x3 problem, fields overridden by kw."""
+    lib = ctypes.CDLL(str(loader.KERNEL_LIB))
+    lib.conv3d_fwd.restype = ctypes.c_int
+    lib.conv3d_last_error.restype = ctypes.c_char_p
+    v = dict(x=0x10000, w=0x20000, bias=0, res=0, out=0x30000, nB=1, D=4, H=6, W=6, C=8, K=8,
+             T=3, R=3, S=3, sd=1, sh=1, sw=1, Z=2, P=4, Q=4, M=32,
+             xs=(4 * 6 * 6 * 8, 6 * 6 * 8, 6 * 8, 8), os=(2 * 4 * 4 * 8, 4 * 4 * 8, 4 * 8, 8),
+             rs=(0, 0, 0, 0))
+    v.update(kw)
+    args = ([ctypes.c_void_p(v[k]) for k in ("x", "w", "bias", "res", "out")]
+            + [ctypes.c_int(v[k]) for k in ("nB", "D", "H", "W", "C", "K", "T", "R", "S", "sd",
+                                             "sh", "sw", "Z", "P", "Q")]
+            + [ctypes.c_long(v["M"])] + [ctypes.c_long(s) for s in (*v["xs"], *v["os"], *v["rs"])]
+            + [ctypes.c_void_p(0)])
+    return lib.conv3d_fwd(*args), lib.conv3d_last_error()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(C=12), b"multiples of 8"),
+    (dict(K=4), b"multiples of 8"),
+    (dict(Z=3), b"VALID"),
+    (dict(M=31), b"nB*Z*P*Q"),
+    (dict(sd=0), b"strides must be positive"),
+    (dict(T=5, D=4), b"VALID"),
+    (dict(x=0x10008), b"aligned"),
+    (dict(bias=0x10004), b"aligned"),
+    (dict(xs=(4 * 6 * 6 * 8, 6 * 6 * 8, 6 * 8, 12)), b"multiples of 8"),
+    (dict(x=0), b"null"),
+    (dict(xs=(1 << 30, 6 * 6 * 8, 6 * 8, 8), nB=2, M=64), b"2^31"),
+])
+def test_conv3d_rejects_without_launch(kw, msg):
+    rc, err = _conv(**kw)
+    assert rc == 1 and msg in err, err
