@@ -49,6 +49,10 @@ def parse_args():
                          "kernel on a 512->512 3x3x3 VAE layer)")
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
                     help="attention input type (profiling; the metric is quoted for fp16)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="instead of attention, measure the sustained fp16 MFMA throughput and "
+                         "shader clock of this GPU on random data, zero data, and random data "
+                         "with the attention kernel's VALU mix (one JSON line)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="instead of attention, time a plain device copy of this many bytes "
                          "(reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -169,11 +173,40 @@ def cpu_baseline():
     }
 
 
+def mfma_ceiling():
+    """Sustained v_mfma_f32_32x32x16_f16 throughput on this GPU (libgfx906_amd_ceiling.so):
+    the card is power-limited under matrix load, so the clock it holds, and with it the
+    reachable TFLOP/s, depends on how much the operands toggle."""
+    import ctypes
+
+    from gfx906_amd.build import CEILING_LIB
+
+    if not CEILING_LIB.is_file():
+        raise RuntimeError(f"{CEILING_LIB} not built; run python -m gfx906_amd.build")
+    lib = ctypes.CDLL(str(CEILING_LIB))
+    lib.mfma_ceiling.restype = ctypes.c_int
+    lib.mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+    res = {}
+    for mode, name in ((1, "zero_data"), (0, "random_data"), (2, "random_data_attn_valu")):
+        tf, ghz = ctypes.c_double(), ctypes.c_double()
+        rc = lib.mfma_ceiling(mode, 4000, 12, ctypes.byref(tf), ctypes.byref(ghz))
+        if rc != 0:
+            raise RuntimeError(f"mfma_ceiling mode {mode} failed with status {rc}")
+        res[name] = {"tflops": round(tf.value, 1), "clock_ghz": round(ghz.value, 3),
+                     "frac_of_peak": round(tf.value / PEAK_TFLOPS, 4)}
+        print(f"mfma ceiling {name}: {tf.value:.1f} TFLOP/s at {ghz.value:.3f} GHz",
+              file=sys.stderr, flush=True)
+    print(json.dumps({"metric": "sustained fp16 MFMA TFLOP/s (v_mfma_f32_32x32x16_f16, "
+                                "2 waves/SIMD, 1 workgroup/CU)",
+                      "unit": "TFLOP/s", "peak": PEAK_TFLOPS, **res}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the attention shards over heads with no communication; see DESIGN.md)",
+              "(the attention shards over heads with no communication)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -185,6 +218,9 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.steps)
+        return
+    if args.ceiling:
+        mfma_ceiling()
         return
 
     if args.workload == "conv3d_vae":

@@ -30,6 +30,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "lib"
 KERNEL_LIB = LIB / "libgfx906_amd_attn.so"
+CEILING_LIB = LIB / "libgfx906_amd_ceiling.so"
 EXT_NAME = "gfx906_amd_attn_ext"
 EXT_LIB = LIB / f"{EXT_NAME}.so"
 
@@ -65,6 +66,15 @@ def build_kernel_lib(extra_flags=()) -> Path:
           *[str(CSRC / f) for f in KERNEL_SOURCES], "-o", str(tmp)])
     os.replace(tmp, KERNEL_LIB)
     return KERNEL_LIB
+
+
+def build_ceiling_lib() -> Path:
+    """Compile the MFMA throughput probe (bench.py --ceiling) into its own library."""
+    LIB.mkdir(exist_ok=True)
+    tmp = CEILING_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *HIP_FLAGS, "-shared", str(CSRC / "mfma_ceiling.hip"), "-o", str(tmp)])
+    os.replace(tmp, CEILING_LIB)
+    return CEILING_LIB
 
 
 def build_extension() -> Path:
@@ -103,6 +113,7 @@ def build_extension() -> Path:
 
 def build_all() -> None:
     build_kernel_lib()
+    build_ceiling_lib()
     build_extension()
 
 

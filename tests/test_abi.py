@@ -207,3 +207,14 @@ def _conv(**kw):
 def test_conv3d_rejects_without_launch(kw, msg):
     rc, err = _conv(**kw)
     assert rc == 1 and msg in err, err
+
+
+def test_mfma_ceiling_library_rejects_bad_arguments_without_launch():
+    from gfx906_amd.build import CEILING_LIB
+
+    lib = ctypes.CDLL(str(CEILING_LIB))
+    lib.mfma_ceiling.restype = ctypes.c_int
+    tf, ghz = ctypes.c_double(), ctypes.c_double()
+    for mode, iters, reps in ((3, 10, 1), (-1, 10, 1), (0, 0, 1), (0, 10, 0)):
+        assert lib.mfma_ceiling(mode, iters, reps, ctypes.byref(tf), ctypes.byref(ghz)) == 1
+    assert lib.mfma_ceiling(0, 10, 1, None, ctypes.byref(ghz)) == 1
