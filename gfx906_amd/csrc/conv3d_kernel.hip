@@ -12,15 +12,21 @@
 //    the A operand of v_mfma_f32_32x32x16_f16, a lane's accumulator holds
 //    four runs of four consecutive output channels of one voxel: the
 //    channels-innermost output, bias and residual move as 8-byte vectors.
-//  * Tiles of 128 channels x 128 voxels x 64 reduction elements, 4 waves of
-//    64x64 (2x2 MFMA blocks). Both operand tiles go from HBM into LDS with
+//  * Tiles of 128 channels x 64*NB voxels x 32 reduction elements (NB = 2, 3
+//    or 4, chosen per problem for how the tile count fills the CUs), 4 waves
+//    of 64 x 32*NB (2 x NB MFMA blocks), two workgroups per CU whose
+//    barriers are independent. Both operand tiles go from HBM into LDS with
 //    buffer loads to LDS (no VGPR staging); the input gather uses a per-lane
-//    offset (voxel base + tap offset from a per-workgroup table), and lanes
-//    past M, K or the reduction length get an out-of-range offset, so the
-//    load returns zeros. LDS rows are 128 bytes with 16-byte units
-//    XOR-swizzled; two stages, loads of k-tile t+1 in flight during t.
+//    offset (voxel base + the offset of the lane's tap, advanced
+//    incrementally from k-tile to k-tile), and lanes past M, K or the
+//    reduction length get an out-of-range offset, so the load returns zeros.
+//    LDS rows are 64 bytes with 16-byte units XOR-swizzled; a ring of three
+//    or four stages keeps the loads of the next k-tiles in flight, k-tiles
+//    past the end load zeros (so every wait count is static), and the
+//    barrier waits for this wave's LDS reads only, not for loads in flight.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "gfx906_amd_conv3d.h"
 
@@ -46,21 +52,42 @@ struct ConvArgs {
 };
 
 constexpr int kBCh = 128;              // output channels per workgroup (GEMM rows)
-constexpr int kBVx = 128;              // output voxels per workgroup (GEMM columns)
-constexpr int kBR = 64;                // reduction elements per k-tile
-constexpr int kNT = 256;               // 4 waves
-constexpr int kRowB = kBR * 2;         // bytes per LDS row: 8 units of 16 bytes
-constexpr int kTile = 128 * kRowB;     // 16 KB: one W or X tile
-constexpr int kStage = 2 * kTile;      // W tile, then X tile
+constexpr int kBR = 32;                // reduction elements per k-tile
+constexpr int kNT = 256;               // 4 waves: 2 along channels x 2 along voxels
+constexpr int kRowB = kBR * 2;         // bytes per LDS row: 4 units of 16 bytes
+constexpr int kWTile = kBCh * kRowB;   // 8 KB: one W tile
 constexpr int kMaxTaps = 1024;
 constexpr unsigned kOOB = 0xFFFFFFF0u;  // buffer offset past any range: loads zeros
 
-// Unit u of LDS row r sits in slot u ^ swz(r). Two 128-byte rows span the 64
+// Per-configuration sizes: NB 32-voxel MFMA blocks per wave (64*NB voxels per
+// workgroup), NST stages in the LDS ring.
+template <int NB, int NST>
+struct ConvCfg {
+    static constexpr int BVX = 64 * NB;            // output voxels per workgroup
+    static constexpr int XTILE = BVX * kRowB;      // bytes of one X tile
+    static constexpr int STAGE = kWTile + XTILE;   // W tile, then X tile
+    static constexpr int LOADS = 2 + NB;           // 1 KB loads per wave per k-tile
+    static constexpr int OCC = 2;                  // workgroups per CU
+    static_assert(NST * STAGE * OCC <= 160 * 1024, "LDS");
+    static_assert(NST >= 3 && NST <= 4, "ring depth");
+};
+
+// Unit u of LDS row r sits in slot u ^ swz(r). Four 64-byte rows span the 64
 // banks, so 16 consecutive rows read at one unit cover 16 different bank
-// groups.
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+// groups: rows r and r+4 differ in swz.
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 #if defined(__HIP_DEVICE_COMPILE__)
+// Workgroup barrier for reusing an LDS stage: this wave's LDS reads are
+// complete (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() there is no
+// release fence: that fence also waits for every outstanding load to LDS
+// (vmcnt(0)), including the k-tiles meant to stay in flight. Each wave waits
+// for its own part of the k-tile to be read (vmcnt(n)) before this.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
 __device__ __forceinline__ f16x8 lds_read16(const char* base, int byte_off) {
     return *(const LDS_AS f16x8*)((const LDS_AS char*)base + byte_off);
 }
@@ -81,38 +108,45 @@ __device__ __forceinline__ Voxel voxel(int m, int Z, int P, int Q) {
 }
 #endif
 
-// grid: (ceil(M / 128), ceil(K / 128)); block: 256 threads.
+// grid: (ceil(M / (64*NB)), ceil(K / 128)); block: 256 threads. SMALLC:
+// C < 32, so that one k-tile can cross several taps.
+template <int NB, int NST, bool SMALLC>
 __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
-    __shared__ int tapoff[kMaxTaps];  // x element offset of tap (t, r, s)
+    using Cf = ConvCfg<NB, NST>;
+    constexpr int STAGE = Cf::STAGE, LOADS = Cf::LOADS;
+    // The ring's stages are separate arrays, so that the compiler can tell
+    // their accesses apart: a read of one stage never waits for the loads
+    // into another.
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st3[NST > 3 ? STAGE : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m0 = blockIdx.x * kBVx, k0 = blockIdx.y * kBCh;
-    const int RS = a.R * a.S, taps = a.T * RS;
-    for (int tp = tid; tp < taps; tp += kNT) {
-        const int t = tp / RS, r = (tp - t * RS) / a.S, s = tp - t * RS - r * a.S;
-        tapoff[tp] = (int)(t * a.xsd + r * a.xsh + s * a.xsw);
-    }
+    const int m0 = blockIdx.x * Cf::BVX, k0 = blockIdx.y * kBCh;
 
-    // Load roles. LDS block b (1 KB, b = wave + 4j) holds rows 8b..8b+7 of a
-    // tile; lane l writes row 8b + l/8, slot l%8, so it fetches unit
-    // u = (l%8) ^ swz(row) = (l%8) ^ ((4(b&1) + l/16) & 7). b&1 = wave&1, so
-    // u is the same in all four of the lane's blocks, and so is the tap of
-    // its reduction group.
-    const int rsub = lane >> 3;
-    const int u = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
-    unsigned wo[4];  // bytes into w (unused, and possibly wrapped, for rows past K)
-    int xo[4];
-    bool wv[4], xv[4];
+    // Load roles. LDS block b (1 KB) holds rows 16b..16b+15 of a tile; lane l
+    // writes row 16b + l/4, slot l%4, so it fetches unit
+    // u = (l%4) ^ swz(row) = (l%4) ^ ((l/16) & 3): the same in all of the
+    // lane's blocks (W blocks wave + 4j, j < 2; X blocks wave + 4j, j < NB),
+    // and so is the tap of its reduction group.
+    const int rsub = lane >> 2;
+    const int u = (lane & 3) ^ ((lane >> 4) & 3);
+    unsigned wo[2];  // bytes into w (unused, and possibly wrapped, for rows past K)
+    bool wv[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = 8 * (wave + 4 * j) + rsub;
-        const int k = k0 + row;
+    for (int j = 0; j < 2; ++j) {
+        const int k = k0 + 16 * (wave + 4 * j) + rsub;
         wv[j] = k < a.K;
         wo[j] = ((unsigned)k * (unsigned)a.KG + 8u * (unsigned)u) * 2u;
-        const int m = m0 + row;
+    }
+    int xo[NB];
+    bool xv[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int m = m0 + 16 * (wave + 4 * j) + rsub;
         xv[j] = m < a.M;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         xo[j] = (int)(v.n * a.xsn + (long long)v.z * a.sd * a.xsd +
@@ -122,85 +156,148 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)a.w_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)a.x_bytes, 0x00020000);
-    __syncthreads();  // tap table ready
 
-    // Loads of the k-tile starting at reduction index i0 into an LDS stage.
-    auto issue = [&](int i0, char* dst) __attribute__((always_inline)) {
-        const int gi = i0 + 8 * u;
+    // The lane's reduction group of the next k-tile to issue: reduction index
+    // gi = i0 + 8u lies in tap (t, r, s) at channel cc, and the tap starts
+    // toff elements into a window (toff = t*xsd + r*xsh + s*xsw). The tap is
+    // advanced incrementally, so the loop reads no tap table.
+    int gi = 8 * u;
+    int cc, ts, tr, toff;
+    {
+        const int tp = gi / a.C;
+        cc = gi - tp * a.C;
+        ts = tp % a.S;
+        tr = (tp / a.S) % a.R;
+        const int tt = tp / (a.S * a.R);
+        toff = (int)(tt * a.xsd + tr * a.xsh + ts * a.xsw);
+    }
+    // Per k-tile the group moves kBR = tstep*C + cstep elements on: whole taps
+    // (C < 32 only), then cstep channels with at most one more tap.
+    const int tstep = SMALLC ? kBR / a.C : 0;
+    const int cstep = kBR - tstep * a.C;
+    const int dr = (int)(a.xsh - a.S * a.xsw), dt = (int)(a.xsd - a.R * a.xsh);
+    // Next tap where `go` holds: s, then r, then t.
+    auto next_tap = [&](bool go) __attribute__((always_inline)) {
+        ts += go ? 1 : 0;
+        toff += go ? (int)a.xsw : 0;
+        const bool ws = ts == a.S;
+        ts = ws ? 0 : ts;
+        tr += ws ? 1 : 0;
+        toff += ws ? dr : 0;
+        const bool wr = tr == a.R;
+        tr = wr ? 0 : tr;
+        toff += wr ? dt : 0;
+    };
+
+    // Loads of the next k-tile (reduction indices i0 .. i0+31) into an LDS
+    // stage, then the lane's group moves on by kBR.
+    int i0 = 0;
+    auto issue = [&](char* dst) __attribute__((always_inline)) {
         const bool kin = gi < a.KG;
-        int toff = 0;
-        if (kin) {
-            const int tp = gi / a.C;
-            toff = tapoff[tp] + (gi - tp * a.C);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const unsigned ow = (wv[j] && kin) ? wo[j] + 2u * (unsigned)i0 : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (LDS_AS void*)(dst + (wave + 4 * j) * 1024), 16, (int)ow, 0, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = wave + 4 * j;
-            const unsigned ow = (wv[j] && kin) ? wo[j] + 2u * (unsigned)i0 : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (LDS_AS void*)(dst + b * 1024), 16, (int)ow,
-                                                     0, 0, 0);
-            const unsigned ox = (xv[j] && kin) ? (unsigned)(2 * (xo[j] + toff)) : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (LDS_AS void*)(dst + kTile + b * 1024), 16,
-                                                     (int)ox, 0, 0, 0);
+        for (int j = 0; j < NB; ++j) {
+            const unsigned ox = (xv[j] && kin) ? (unsigned)(2 * (xo[j] + toff + cc)) : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (LDS_AS void*)(dst + kWTile + (wave + 4 * j) * 1024), 16, (int)ox, 0, 0, 0);
         }
+        i0 += kBR;
+        gi += kBR;
+        if (SMALLC) {  // tstep <= 4 for C >= 8
+#pragma unroll
+            for (int i = 0; i < 4; ++i) next_tap(i < tstep);
+        }
+        cc += cstep;
+        const bool wrap = cc >= a.C;
+        cc -= wrap ? a.C : 0;
+        next_tap(wrap);
     };
 
     // MFMA operand addresses: lane l reads row (32-row block base + l%32),
     // unit 2*ks + l/32 (16 reduction elements per k-step).
     const int g = lane >> 5, r32 = lane & 31;
     const int wch = wave & 1, wvx = wave >> 1;  // channel half, voxel half
-    int aaddr[2][4], baddr[2][4];
+    int aaddr[2][2], baddr[NB][2];
 #pragma unroll
-    for (int bl = 0; bl < 2; ++bl)
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int ra = wch * 64 + bl * 32 + r32, rb = wvx * 64 + bl * 32 + r32;
+        for (int bl = 0; bl < 2; ++bl) {
+            const int ra = wch * 64 + bl * 32 + r32;
             aaddr[bl][ks] = ra * kRowB + (((2 * ks + g) ^ swz(ra)) * 16);
-            baddr[bl][ks] = rb * kRowB + (((2 * ks + g) ^ swz(rb)) * 16);
         }
+#pragma unroll
+        for (int bl = 0; bl < NB; ++bl) {
+            const int rb = wvx * 32 * NB + bl * 32 + r32;
+            baddr[bl][ks] = kWTile + rb * kRowB + (((2 * ks + g) ^ swz(rb)) * 16);
+        }
+    }
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][NB];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb) acc[cb][vb] = f32x16{};
+        for (int vb = 0; vb < NB; ++vb) acc[cb][vb] = f32x16{};
 
-    // The stage pointers are restrict-qualified: the stage being filled and
-    // the stage being read are disjoint, so reads need not wait for the loads.
-    const int nkt = (a.KG + kBR - 1) / kBR;
-    auto step = [&](int kt, char* __restrict__ nxt, const char* __restrict__ cur)
+    // One k-tile from stage cur, after issuing the loads of the k-tile NST-1
+    // ahead into fill (the stage of the k-tile before this one).
+    auto step = [&](char* __restrict__ fill, const char* __restrict__ cur)
         __attribute__((always_inline)) {
-        if (kt + 1 < nkt) issue((kt + 1) * kBR, nxt);
-        const char* sw = cur;
-        const char* sx = cur + kTile;
+        // vmcnt(NST-2 k-tiles of loads): this wave's part of the k-tile in cur
+        // landed.
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((NST - 2) * LOADS));
+        lds_barrier();    // every wave's; the k-tile in fill was consumed
+        issue(fill);
+        f16x8 af[2][2], bf[2][NB];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            f16x8 af[2], bf[2];
+        for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-            for (int bl = 0; bl < 2; ++bl) {
-                af[bl] = lds_read16(sw, aaddr[bl][ks]);
-                bf[bl] = lds_read16(sx, baddr[bl][ks]);
-            }
+            for (int bl = 0; bl < 2; ++bl) af[ks][bl] = lds_read16(cur, aaddr[bl][ks]);
+#pragma unroll
+            for (int bl = 0; bl < NB; ++bl) bf[ks][bl] = lds_read16(cur, baddr[bl][ks]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int vb = 0; vb < 2; ++vb)
-                    acc[cb][vb] =
-                        __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cb], bf[vb], acc[cb][vb], 0, 0, 0);
-        }
+                for (int vb = 0; vb < NB; ++vb)
+                    acc[cb][vb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks][cb], bf[ks][vb],
+                                                                         acc[cb][vb], 0, 0, 0);
     };
-    issue(0, lds);
-    for (int kt = 0; kt < nkt; ++kt) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of k-tile kt landed
-        __syncthreads();                    // every wave's; k-tile kt-1's stage is free
-        step(kt, lds + ((kt + 1) & 1) * kStage, lds + (kt & 1) * kStage);
+    // k-tile t sits in stage t % NST. The loop runs whole groups of NST
+    // k-tiles: k-tiles past the end load zeros and add nothing.
+    const int nkt = (a.KG + kBR - 1) / kBR;
+    issue(st0);
+    issue(st1);
+    if constexpr (NST == 4) {
+        issue(st2);
+        for (int kt = 0; kt < nkt; kt += 4) {
+            step(st3, st0);
+            step(st0, st1);
+            step(st1, st2);
+            step(st2, st3);
+        }
+    } else {
+        for (int kt = 0; kt < nkt; kt += 3) {
+            step(st2, st0);
+            step(st0, st1);
+            step(st1, st2);
+        }
     }
+    // The zero loads past the last k-tile must land before the workgroup's
+    // LDS is released.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
 
     // Epilogue: accumulator row 8(r/4) + 4g + r%4 (an output channel), column
     // l%32 (an output voxel); four runs of four channels per lane and voxel.
 #pragma unroll
-    for (int vb = 0; vb < 2; ++vb) {
-        const int m = m0 + wvx * 64 + vb * 32 + r32;
+    for (int vb = 0; vb < NB; ++vb) {
+        const int m = m0 + wvx * 32 * NB + vb * 32 + r32;
         if (m >= a.M) continue;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         const long long oo = v.n * a.osn + v.z * a.osz + v.p * a.osp + v.q * a.osq;
@@ -221,6 +318,17 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 #endif
 }
 
+// Launches configuration (NB, NST) over the whole problem.
+template <int NB, int NST>
+void launch_cfg(const ConvArgs& a, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + ConvCfg<NB, NST>::BVX - 1) / ConvCfg<NB, NST>::BVX),
+              (unsigned)((a.K + kBCh - 1) / kBCh));
+    if (a.C < kBR)
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, true>), grid, dim3(kNT), 0, stream, a);
+    else
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, false>), grid, dim3(kNT), 0, stream, a);
+}
+
 thread_local char g_err[256];
 
 void set_err(const char* msg) {
@@ -235,6 +343,42 @@ int fail(const char* msg) {
 }
 
 bool mult8(long v) { return v >= 0 && v % 8 == 0; }
+
+// Voxel-tile width (NB 32-voxel blocks per wave, 64*NB voxels per workgroup)
+// for an M x K problem. Wider tiles read fewer LDS bytes and pass fewer
+// barriers per MFMA; narrower ones fill the CUs better when the tile count is
+// small or just past a multiple of the workgroup slots (2 per CU). Estimated
+// time: workgroup rounds at half-round granularity (a CU running a single
+// workgroup finishes it sooner) x tile width x relative cost per voxel,
+// measured on MI355X as 1.19 / 1.05 / 1.0 for NB = 2 / 3 / 4.
+// GFX906_AMD_CONV_NB = 2, 3 or 4 overrides the choice (testing).
+int pick_nb(long M, int K) {
+    const char* e = getenv("GFX906_AMD_CONV_NB");
+    const int forced = e ? atoi(e) : 0;
+    if (forced >= 2 && forced <= 4) return forced;
+    static const int slots = [] {
+        int dev = 0, ncu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            ncu <= 0)
+            ncu = 256;
+        return 2 * ncu;
+    }();
+    const double rel[5] = {0, 0, 1.19, 1.05, 1.0};
+    const long kt = (K + kBCh - 1) / kBCh;
+    int best = 4;
+    double best_cost = 1e300;
+    for (int nb = 4; nb >= 2; --nb) {
+        const long tiles = (M + 64 * nb - 1) / (64 * nb) * kt;
+        const double halves = (double)((2 * tiles + slots - 1) / slots);
+        const double cost = halves * nb * rel[nb];
+        if (cost < best_cost * 0.999) {
+            best_cost = cost;
+            best = nb;
+        }
+    }
+    return best;
+}
 
 }  // namespace
 
@@ -301,8 +445,13 @@ extern "C" int conv3d_fwd(const void* x, const void* w, const void* bias, const 
     a.rsq = rsq;
     a.x_bytes = (unsigned)x_span;
     a.w_bytes = (unsigned)w_span;
-    dim3 grid((unsigned)((M + kBVx - 1) / kBVx), (unsigned)((K + kBCh - 1) / kBCh));
-    hipLaunchKernelGGL(conv3d_mfma, grid, dim3(kNT), 0, stream, a);
+    const int nb = pick_nb(M, K);
+    if (nb == 2)
+        launch_cfg<2, 4>(a, stream);
+    else if (nb == 3)
+        launch_cfg<3, 4>(a, stream);
+    else
+        launch_cfg<4, 3>(a, stream);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
