@@ -112,17 +112,19 @@ def vae_attn(q, k, v, fallback):
         return fallback(q, k, v)
     b, c, h, w = q.shape
 
-    def tokens(x):  # [b, c, h, w] -> [b, 1, h*w, c]: a view with strided channels,
-        # which the binding copies (the kernel reads a contiguous head dim)
+    def tokens(x):  # [b, c, h, w] -> [b, 1, h*w, c]: a token-contiguous view (sequence
+        # stride 1, channel stride h*w); the op transposes it (faster on gfx950 than
+        # the in-place kernel) and fills the [b, c, h, w] output through its view
         return x.reshape(b, c, h * w).transpose(1, 2).unsqueeze(1)
 
+    out = torch.empty((b, c, h, w), dtype=q.dtype, device=q.device)
     try:
-        out = mod.attn(tokens(q), tokens(k), tokens(v), c ** -0.5)
+        mod.attn(tokens(q), tokens(k), tokens(v), c ** -0.5, out=tokens(out))
     except Exception:  # noqa: BLE001 - a VAE decode must not fail on the fast path
         logger.warning("gfx950 VAE attention failed; using %s",
                        getattr(fallback, "__name__", fallback))
         return fallback(q, k, v)
-    return out.squeeze(1).transpose(1, 2).reshape(b, c, h, w)
+    return out
 
 
 def install_vae_hook() -> None:

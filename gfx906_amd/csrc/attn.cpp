@@ -14,12 +14,19 @@
 //  * Strided inputs are read in place when the head dim is contiguous and
 //    the other strides are multiples of 8 elements (16-byte aligned data);
 //    only other layouts are copied, where the reference always calls
-//    .contiguous() (attn.cpp:15).
+//    .contiguous() (attn.cpp:15). The VAE's token-contiguous views
+//    ([b, c, h*w] seen as [b, 1, h*w, c], deploy/gfx906_attention.py:102-104)
+//    are copied too, on purpose: the kernel that reads them in place
+//    (attn_fwd_ex with their strides) needs transposing LDS reads for K and
+//    is slower on gfx950 than a transpose copy plus the contiguous kernel
+//    (1.42 against 1.18 ms at h*w = 16384).
 //  * `out`, if given, is written instead of allocating: any [B, H, Sq, D]
-//    view of q's dtype and device with a contiguous head dim and
-//    non-overlapping rows, e.g. the transpose of a [B, Sq, H, D] buffer. It
-//    must not overlap k or v (every workgroup of a head reads them); it may
-//    be q itself (a workgroup reads its own query rows before writing them).
+//    view of q's dtype and device whose elements do not overlap, e.g. the
+//    transpose of a [B, Sq, H, D] buffer; a view with a strided head dim
+//    (the VAE's [b, 1, h*w, c] view of a [b, c, h, w] output) is filled
+//    through a contiguous temporary. It must not overlap k or v (every
+//    workgroup of a head reads them); it may be q itself (a workgroup reads
+//    its own query rows before writing them).
 //  * Checks raising RuntimeError: k and v must match q's dtype and device,
 //    sizes must fit the kernel's indexing, and a launch error is reported
 //    instead of being dropped.
@@ -32,11 +39,12 @@
 
 namespace {
 
-// Element strides {batch, head, seq} of a 4-D tensor (0 for size-1 dims,
-// whose stride is never used).
-std::array<long long, 3> strides3(const torch::Tensor& t) {
-    std::array<long long, 3> s;
+// Element strides {batch, head, seq, head dim} of a 4-D tensor (0 for size-1
+// batch/head/seq dims, whose stride is never used).
+std::array<long long, 4> strides4(const torch::Tensor& t) {
+    std::array<long long, 4> s;
     for (int d = 0; d < 3; ++d) s[d] = t.size(d) == 1 ? 0 : t.stride(d);
+    s[3] = t.stride(3);
     return s;
 }
 
@@ -46,9 +54,10 @@ std::array<long long, 3> strides3(const torch::Tensor& t) {
 bool readable_in_place(const torch::Tensor& t, bool kv) {
     if (t.stride(3) != 1) return false;
     if (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) return false;
-    for (long long s : strides3(t))
-        if (s < 0 || s % 8) return false;
-    return !kv || strides3(t)[2] <= (1 << 24);
+    const auto s = strides4(t);
+    for (int d = 0; d < 3; ++d)
+        if (s[d] < 0 || s[d] % 8) return false;
+    return !kv || s[2] <= (1 << 24);
 }
 
 torch::Tensor as_input(const torch::Tensor& t, bool kv) {
@@ -84,19 +93,25 @@ torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double sca
         TORCH_CHECK(o.dim() == 4 && o.size(0) == B && o.size(1) == H && o.size(2) == Sq &&
                         o.size(3) == D,
                     "kernel: out must be [B, H, Sq, D]");
-        TORCH_CHECK(o.stride(3) == 1, "kernel: out must have a contiguous head dim");
     } else {
         o = torch::empty({B, H, Sq, D}, q.options().memory_format(at::MemoryFormat::Contiguous));
     }
     if (o.numel() == 0) return o;
+    // The head dim of every tensor the kernel touches is contiguous: inputs
+    // are copied and out staged as needed.
     const auto qi = as_input(q, false), ki = as_input(k, true), vi = as_input(v, true);
-    const auto sq = strides3(qi), sk = strides3(ki), sv = strides3(vi), so = strides3(o);
+    const bool staged = o.stride(3) != 1;
+    torch::Tensor oo =
+        staged ? torch::empty({B, H, Sq, D}, q.options().memory_format(at::MemoryFormat::Contiguous))
+               : o;
+    const auto sq = strides4(qi), sk = strides4(ki), sv = strides4(vi), so = strides4(oo);
     const int dtype = q.dtype() == torch::kBFloat16 ? ATTN_DTYPE_BF16 : ATTN_DTYPE_F16;
-    const int rc = attn_fwd_ex(qi.data_ptr(), ki.data_ptr(), vi.data_ptr(), o.data_ptr(), (int)B,
+    const int rc = attn_fwd_ex(qi.data_ptr(), ki.data_ptr(), vi.data_ptr(), oo.data_ptr(), (int)B,
                                (int)H, (int)Sq, (int)Skv, (int)D, (float)scale,
                                c10::hip::getCurrentHIPStream().stream(), dtype, sq.data(),
                                sk.data(), sv.data(), so.data());
     TORCH_CHECK(rc == 0, "kernel: ", attn_last_error() ? attn_last_error() : "launch failed");
+    if (staged) o.copy_(oo);
     return o;
 }
 

@@ -75,10 +75,11 @@ constexpr float kPmaxLimit = 256.0f;  // 2^kTau
 // sched_group_barrier instruction classes
 constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
 
-// Strides of one tensor in elements: batch, head, sequence (the head dim is
-// contiguous).
-struct Strides3 {
-    long long b, h, s;
+// Strides of one tensor in elements: batch, head, sequence, head dim. The
+// head dim is contiguous (d == 1) except in the token-contiguous D = 512
+// layout (attn_fwd_d512<T, true>).
+struct Strides {
+    long long b, h, s, d;
 };
 
 // Kernel arguments. c = |scale| * log2(e) (at least 1e-30); qsign < 0 for a
@@ -88,7 +89,7 @@ struct KArgs {
     const void* k;
     const void* v;
     void* o;
-    Strides3 sq, sk, sv, so;
+    Strides sq, sk, sv, so;
     int H, Sq, Skv, D;
     float c, qsign;
 };
@@ -588,6 +589,30 @@ struct Cfg512 {
     static constexpr int NLD = BN / NW;  // rows loaded per wave per tile, per tensor
 };
 
+// Token-contiguous layout (k and v with sequence stride 1, the head dim
+// strided: the VAE's [b, c, h*w] activations seen as [b, 1, h*w, c]). A tile
+// arrives as K^T and V^T, 512 dim rows of 32 keys (64 bytes) each, through the
+// same direct loads; 16-byte chunk c of row r sits in slot c ^ tswz(r). The
+// keys of the score blocks are permuted (tkey) so that each lane's P holds 8
+// consecutive keys, making a V^T fragment one 16-byte read, while the
+// transposed K reads of the two 16-lane groups served together fall on
+// complementary 8-byte halves of the slots: both read patterns are free of
+// bank conflicts.
+struct Cfg512T {
+    static constexpr int ROWB = Cfg512::BN * 2;    // 64 bytes: one dim row of a tile
+    static constexpr int TILE = Cfg512::DP * ROWB;  // 32 KB: K^T or V^T of one tile
+    static constexpr int STAGE = 2 * TILE;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int LPW = TILE / 1024 / Cfg512::NW;  // 1 KB loads per wave, tensor, tile
+};
+
+// Slot swizzle of the token-contiguous tiles: bit 2 of the row to bit 1 of
+// the slot, bit 3 to bit 0.
+__host__ __device__ constexpr int tswz(int r) { return (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+// Key held in row 4j + t of score block kb (j, t < 4) in the token-contiguous
+// kernel: lane group g's rows of blocks 0 and 1 are keys 8g..8g+7.
+__host__ __device__ constexpr int tkey(int kb, int j, int t) { return 8 * j + 4 * ((j + kb) & 1) + t; }
+
 #if defined(__HIP_DEVICE_COMPILE__)
 // Rare path of the D = 512 kernel: the tile's scores exceed the running max by
 // more than kTau. Returns the new max, the rescale factor for O and l, and P
@@ -624,8 +649,10 @@ __device__ __attribute__((noinline)) Rescale512<T> d512_rescale(f32x4 S0, f32x4 
 }
 #endif
 
-// grid: ceil(Sq / 128) * B*H workgroups; block: 512 threads.
-template <class T>
+// grid: ceil(Sq / 128) * B*H workgroups; block: 512 threads. TL: k and v in
+// the token-contiguous layout (Cfg512T), q and o read and written element by
+// element with any strides.
+template <class T, bool TL>
 __global__ void __launch_bounds__(Cfg512::NT, 1)
 attn_fwd_d512(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -636,7 +663,9 @@ attn_fwd_d512(const KArgs a) {
     static_assert(NLD * C::NW == BN && D * 2 == 64 * 16, "one row per load instruction");
     constexpr int NQF = D / 32;  // Q fragments (32 dims each)
     constexpr int NOB = D / 16;  // 16-dim output blocks
-    __shared__ __attribute__((aligned(1024))) char lds[C::LDS];  // 2 stages x (K, V)
+    constexpr int STAGE = TL ? Cfg512T::STAGE : C::STAGE;
+    constexpr int VOFF = TL ? Cfg512T::TILE : C::KTILE;  // V (V^T) tile within a stage
+    __shared__ __attribute__((aligned(1024))) char lds[TL ? Cfg512T::LDS : C::LDS];  // 2 x (K, V)
 
     const int Sq = a.Sq, Skv = a.Skv;
     const float c = a.c;
@@ -655,11 +684,45 @@ attn_fwd_d512(const KArgs a) {
     const int qrow = qt * C::BM + wave * 16 + i;
     const bool live = qrow < Sq;
 
-    auto stage = [&](int t) { return lds + (t & 1) * C::STAGE; };
+    auto stage = [&](int t) { return lds + (t & 1) * STAGE; };
     // Direct loads: one instruction per K or V row; lane l fetches dims
     // 8l..8l+7. Rows past Skv read as zeros (the descriptor covers the valid
     // rows only).
+    // Token-contiguous layout: lane l of 1 KB block j writes dim row
+    // 16j + l/4, slot l%4, so it fetches key chunk tu = (l%4) ^ tswz(row),
+    // the same in every block; chunks at or past Skv load zeros. Byte offsets
+    // of the lane's rows at key 0 (the host keeps them below 2^31).
+    const int tu = (lane & 3) ^ ((((lane >> 4) & 1) << 1) | ((lane >> 5) & 1));
+    unsigned ktrow[TL ? Cfg512T::LPW : 1], vtrow[TL ? Cfg512T::LPW : 1];
+    __amdgpu_buffer_rsrc_t rkt, rvt;
+    if constexpr (TL) {
+#pragma unroll
+        for (int n = 0; n < Cfg512T::LPW; ++n) {
+            const long long row = 16 * (wave + n * C::NW) + (lane >> 2);
+            ktrow[n] = (unsigned)((row * a.sk.d + 8 * tu) * 2);
+            vtrow[n] = (unsigned)((row * a.sv.d + 8 * tu) * 2);
+        }
+        const int kb = __builtin_amdgcn_readfirstlane((int)(((D - 1) * a.sk.d + Skv) * 2));
+        const int vb = __builtin_amdgcn_readfirstlane((int)(((D - 1) * a.sv.d + Skv) * 2));
+        rkt = __builtin_amdgcn_make_buffer_rsrc((void*)Kh, 0, kb, 0x00020000);
+        rvt = __builtin_amdgcn_make_buffer_rsrc((void*)Vh, 0, vb, 0x00020000);
+    }
     auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
+        if constexpr (TL) {
+            const int k0 = t * BN;
+            const bool kin = k0 + 8 * tu < Skv;
+#pragma unroll
+            for (int n = 0; n < Cfg512T::LPW; ++n) {
+                const int blk = wave + n * C::NW;
+                const unsigned ok = kin ? ktrow[n] + 2u * (unsigned)k0 : 0xFFFFFFF0u;
+                const unsigned ov = kin ? vtrow[n] + 2u * (unsigned)k0 : 0xFFFFFFF0u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rkt, (LDS_AS void*)(dst + blk * 1024), 16,
+                                                         (int)ok, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rvt, (LDS_AS void*)(dst + Cfg512T::TILE + blk * 1024), 16, (int)ov, 0, 0, 0);
+            }
+            return;
+        }
         const int rows = min(Skv - t * BN, BN);
         const int kbytes = (int)(((rows - 1) * kss + D) * 2);
         const int vbytes = (int)(((rows - 1) * vss + D) * 2);
@@ -683,14 +746,37 @@ attn_fwd_d512(const KArgs a) {
     x8 qf[NQF];
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int s = 0; s < NQF; ++s)
-        qf[s] = q_fragment(Qh + qrow * a.sq.s + 32 * s + 8 * g, live, qneg);
+    for (int s = 0; s < NQF; ++s) {
+        if constexpr (TL) {  // any strides: eight element loads
+            x8 val = {};
+            if (live)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) val[e] = Qh[qrow * a.sq.s + (32 * s + 8 * g + e) * a.sq.d];
+            qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(u32x4, val) ^ qneg);
+        } else {
+            qf[s] = q_fragment(Qh + qrow * a.sq.s + 32 * s + 8 * g, live, qneg);
+        }
+    }
 
     // K read: row kb*16 + i, dims 32s + 8g.. ; V^T read (transposed, per
     // 16-lane group g): row 4g + i/4 (+16 for the second key half), dims
     // 16*db + 4*(i%4)..
     const int kbase = i * C::KS + g * 16;
     const int vbase = (4 * g + (i >> 2)) * C::VS + 8 * (i & 3);
+    // Token-contiguous layout. K^T read (ds_read_b64_tr_b16, two per
+    // fragment, h = 0, 1): lane 4e + j of group g reads keys tkey(kb, j, 0..3)
+    // of dim row 32s + 8g + 4h + e (chunk j, half (j + kb) & 1; the row's
+    // swizzle is tswz = 2h + g%2), so lane i receives key tkey(kb, i/4, i%4),
+    // dims 32s + 8g + 4h + 0..3. V^T read: dim row 16ob + i, keys 8g..8g+7
+    // (chunk g), one 16-byte read.
+    int ktb[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+            ktb[h][kb] = (8 * g + 4 * h + (i >> 2)) * Cfg512T::ROWB +
+                         (((i & 3) ^ ((h << 1) | (g & 1))) * 16) + (((i & 3) + kb) & 1) * 8;
+    const int vtb = i * Cfg512T::ROWB + ((g ^ tswz(i)) * 16);
 
     f32x4 oacc[NOB];
 #pragma unroll
@@ -719,14 +805,19 @@ attn_fwd_d512(const KArgs a) {
         __attribute__((always_inline)) {
         if (t + 1 < ntiles) issue(t + 1, nxt);
         const char* sk = cur;
-        const char* sv = cur + C::KTILE;
+        const char* sv = cur + VOFF;
         f32x4 S[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             f32x4 Sp[2] = {f32x4{}, f32x4{}};
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
-                const x8 kf = lds_read16<T>(sk, kbase + kb * 16 * C::KS + s * 64);
+                x8 kf;
+                if constexpr (TL)
+                    kf = lds_read_tr2<T>(sk, ktb[0][kb] + s * 32 * Cfg512T::ROWB,
+                                         ktb[1][kb] + s * 32 * Cfg512T::ROWB);
+                else
+                    kf = lds_read16<T>(sk, kbase + kb * 16 * C::KS + s * 64);
                 Sp[s & 1] = E::mma16(kf, qf[s], Sp[s & 1]);
             }
             __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
@@ -742,8 +833,10 @@ attn_fwd_d512(const KArgs a) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (t * BN + kb * 16 + 4 * g + r >= Skv) S[kb][r] = -INFINITY;
+                for (int r = 0; r < 4; ++r) {
+                    const int key = TL ? tkey(kb, g, r) : kb * 16 + 4 * g + r;
+                    if (t * BN + key >= Skv) S[kb][r] = -INFINITY;
+                }
         }
         if (t == 0) {  // first tile: start from its exact max (O is still zero)
             float mx = fmaxf(max3(S[0][0], S[0][1], S[0][2]), max3(S[0][3], S[1][0], S[1][1]));
@@ -770,10 +863,20 @@ attn_fwd_d512(const KArgs a) {
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) oacc[ob] *= alpha;
         l_run += l_tile;
+        if constexpr (TL) {  // odd lane groups: block 1 holds keys 8g..8g+3
+            const u32x4 pw = __builtin_bit_cast(u32x4, P);
+            const bool sw = g & 1;
+            P = __builtin_bit_cast(x8, u32x4{sw ? pw[2] : pw[0], sw ? pw[3] : pw[1],
+                                             sw ? pw[0] : pw[2], sw ? pw[1] : pw[3]});
+        }
         // O^T += V^T P^T, one 16x16x32 MFMA per 16-dim block.
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) {
-            const x8 vf = lds_read_tr2<T>(sv, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
+            x8 vf;
+            if constexpr (TL)
+                vf = lds_read16<T>(sv, vtb + ob * 16 * Cfg512T::ROWB);
+            else
+                vf = lds_read_tr2<T>(sv, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
             oacc[ob] = E::mma16(vf, P, oacc[ob]);
         }
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, 4, 0);
@@ -794,13 +897,20 @@ attn_fwd_d512(const KArgs a) {
     const float l = quad_group_sum(l_run);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (live) {
-        T* op = Oh + qrow * a.so.s + 4 * g;
+        T* op = Oh + qrow * a.so.s;
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) {
             const auto h0 = E::cvt2(oacc[ob][0] * inv, oacc[ob][1] * inv);
             const auto h1 = E::cvt2(oacc[ob][2] * inv, oacc[ob][3] * inv);
-            *reinterpret_cast<typename E::x4*>(op + 16 * ob) =
-                typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+            const int d0 = 16 * ob + 4 * g;
+            if constexpr (TL) {  // any strides: four element stores
+                op[(d0 + 0) * a.so.d] = h0[0];
+                op[(d0 + 1) * a.so.d] = h0[1];
+                op[(d0 + 2) * a.so.d] = h1[0];
+                op[(d0 + 3) * a.so.d] = h1[1];
+            } else {
+                *reinterpret_cast<typename E::x4*>(op + d0) = typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+            }
         }
     }
 #endif
@@ -818,11 +928,14 @@ using Cfg128 = Cfg<128, 8, 1, 1>;  // 128 KB of LDS: one workgroup, two waves pe
 using Cfg64 = Cfg<64, 8, 1, 2>;    // 64 KB: two workgroups, four waves per SIMD
 
 template <class T>
-hipError_t launch_t(const KArgs& a, int BH, hipStream_t s) {
+hipError_t launch_t(const KArgs& a, int BH, bool tl, hipStream_t s) {
     const int D = a.D;
     if (D == 512) {
         dim3 grid((unsigned)((a.Sq + Cfg512::BM - 1) / Cfg512::BM) * (unsigned)BH);
-        hipLaunchKernelGGL((attn_fwd_d512<T>), grid, dim3(Cfg512::NT), 0, s, a);
+        if (tl)
+            hipLaunchKernelGGL((attn_fwd_d512<T, true>), grid, dim3(Cfg512::NT), 0, s, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_d512<T, false>), grid, dim3(Cfg512::NT), 0, s, a);
     } else if (D == 128) {
         dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * (unsigned)BH);
         hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T>), grid, dim3(Cfg128::NT), 0, s, a);
@@ -836,15 +949,14 @@ hipError_t launch_t(const KArgs& a, int BH, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Whether the rows of an output tensor can overlap: the (stride, size)
-// pairs of its batch, head and sequence dims, sorted by stride, must each
-// step past everything the smaller ones span (innermost: D contiguous
-// elements). Dims of size 1 are ignored.
-bool output_overlaps(const Strides3& s, int B, int H, int Sq, int D) {
-    long long st[3] = {s.b, s.h, s.s};
-    long long n[3] = {B, H, Sq};
-    for (int i = 0; i < 3; ++i)
-        for (int j = i + 1; j < 3; ++j)
+// Whether two elements of an output tensor can share an address: the
+// (stride, size) pairs of its four dims, sorted by stride, must each step
+// past everything the smaller ones span. Dims of size 1 are ignored.
+bool output_overlaps(const Strides& s, int B, int H, int Sq, int D) {
+    long long st[4] = {s.b, s.h, s.s, s.d};
+    long long n[4] = {B, H, Sq, D};
+    for (int i = 0; i < 4; ++i)
+        for (int j = i + 1; j < 4; ++j)
             if (st[j] < st[i]) {
                 long long t = st[i];
                 st[i] = st[j];
@@ -853,8 +965,8 @@ bool output_overlaps(const Strides3& s, int B, int H, int Sq, int D) {
                 n[i] = n[j];
                 n[j] = t;
             }
-    long long extent = D;
-    for (int i = 0; i < 3; ++i) {
+    long long extent = 1;
+    for (int i = 0; i < 4; ++i) {
         if (n[i] <= 1) continue;
         if (st[i] < extent) return true;
         extent = st[i] * (n[i] - 1) + extent;
@@ -862,61 +974,72 @@ bool output_overlaps(const Strides3& s, int B, int H, int Sq, int D) {
     return false;
 }
 
+// Whether k and v use the token-contiguous D = 512 layout: sequence stride 1
+// (so a 32-key run of one dim is 64 contiguous bytes) and a strided head dim.
+bool token_contiguous(const Strides& sk, const Strides& sv, int D) {
+    return D == 512 && sk.s == 1 && sv.s == 1 && sk.d != 1 && sv.d != 1;
+}
+
+int fail(const char* msg) {
+    set_err(msg);
+    return 1;
+}
+
 // Validates the arguments; returns 0, or 1 with the error message set.
 int check_args(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
-               int Skv, int D, int dtype, const Strides3& sq, const Strides3& sk,
-               const Strides3& sv, const Strides3& so) {
-    if (B < 0 || H < 0 || Sq < 0 || Skv < 0) {
-        set_err("attn: negative size");
-        return 1;
-    }
-    if (!((D <= 64 && D > 0 && D % 8 == 0) || D == 128 || D == 512)) {
-        set_err("attn: head_dim must be <=64 and a multiple of 8, or 128, or 512");
-        return 1;
-    }
-    if (dtype != ATTN_DTYPE_F16 && dtype != ATTN_DTYPE_BF16) {
-        set_err("attn: dtype must be ATTN_DTYPE_F16 or ATTN_DTYPE_BF16");
-        return 1;
-    }
-    if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL || (long)B * H > 65535) {
-        set_err("attn: grid too large");
-        return 1;
-    }
+               int Skv, int D, int dtype, const Strides& sq, const Strides& sk,
+               const Strides& sv, const Strides& so) {
+    if (B < 0 || H < 0 || Sq < 0 || Skv < 0) return fail("attn: negative size");
+    if (!((D <= 64 && D > 0 && D % 8 == 0) || D == 128 || D == 512))
+        return fail("attn: head_dim must be <=64 and a multiple of 8, or 128, or 512");
+    if (dtype != ATTN_DTYPE_F16 && dtype != ATTN_DTYPE_BF16)
+        return fail("attn: dtype must be ATTN_DTYPE_F16 or ATTN_DTYPE_BF16");
+    if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL || (long)B * H > 65535)
+        return fail("attn: grid too large");
     if (B == 0 || H == 0 || Sq == 0) return 0;
-    if (!q || !o || (Skv > 0 && (!k || !v))) {
-        set_err("attn: null pointer");
-        return 1;
+    if (!q || !o || (Skv > 0 && (!k || !v))) return fail("attn: null pointer");
+    const Strides* all[4] = {&sq, &sk, &sv, &so};
+    for (const Strides* s : all)
+        if (s->b < 0 || s->h < 0 || s->s < 0 || s->d < 0)
+            return fail("attn: strides must be non-negative");
+    if (token_contiguous(sk, sv, D)) {
+        // k, v: direct loads of 16-byte key runs; q, o: element access.
+        const Strides* kv[2] = {&sk, &sv};
+        for (const Strides* s : kv)
+            if (s->b % 8 || s->h % 8 || s->d % 8)
+                return fail("attn: token-contiguous k/v need batch/head/dim strides that are "
+                            "multiples of 8 elements");
+        if (((uintptr_t)k | (uintptr_t)v) % 16 || ((uintptr_t)q | (uintptr_t)o) % 2)
+            return fail("attn: token-contiguous k/v must be 16-byte aligned");
+        if (Skv % 8) return fail("attn: token-contiguous k/v need Skv % 8 == 0");
+        if ((long long)(D - 1) * sk.d + Skv >= (1LL << 30) ||
+            (long long)(D - 1) * sv.d + Skv >= (1LL << 30))
+            return fail("attn: token-contiguous k/v span 2^30 elements or more per head");
+        if (output_overlaps(so, B, H, Sq, D)) return fail("attn: o strides make output elements overlap");
+        return 0;
     }
+    if (sq.d != 1 || sk.d != 1 || sv.d != 1 || so.d != 1)
+        return fail("attn: the head dim must be contiguous (stride 1), except for D == 512 with "
+                    "token-contiguous k and v");
     // 16-byte vector loads of q, k, v and 8-byte stores of o.
-    const Strides3* in[3] = {&sq, &sk, &sv};
-    for (const Strides3* s : in)
-        if (s->b < 0 || s->h < 0 || s->s < 0 || s->b % 8 || s->h % 8 || s->s % 8) {
-            set_err("attn: q/k/v strides must be non-negative multiples of 8 elements");
-            return 1;
-        }
-    if (so.b < 0 || so.h < 0 || so.s < 0 || so.b % 4 || so.h % 4 || so.s % 4) {
-        set_err("attn: o strides must be non-negative multiples of 4 elements");
-        return 1;
-    }
-    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 || (uintptr_t)o % 8) {
-        set_err("attn: q/k/v must be 16-byte and o 8-byte aligned");
-        return 1;
-    }
+    const Strides* in[3] = {&sq, &sk, &sv};
+    for (const Strides* s : in)
+        if (s->b % 8 || s->h % 8 || s->s % 8)
+            return fail("attn: q/k/v strides must be non-negative multiples of 8 elements");
+    if (so.b % 4 || so.h % 4 || so.s % 4)
+        return fail("attn: o strides must be non-negative multiples of 4 elements");
+    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 || (uintptr_t)o % 8)
+        return fail("attn: q/k/v must be 16-byte and o 8-byte aligned");
     // K/V tile offsets and buffer ranges are 32-bit: 64 rows of the sequence
     // stride must stay below 2^31 bytes.
-    if (sk.s > (1 << 24) || sv.s > (1 << 24)) {
-        set_err("attn: k/v sequence stride above 2^24 elements");
-        return 1;
-    }
-    if (output_overlaps(so, B, H, Sq, D)) {
-        set_err("attn: o strides make output rows overlap");
-        return 1;
-    }
+    if (sk.s > (1 << 24) || sv.s > (1 << 24))
+        return fail("attn: k/v sequence stride above 2^24 elements");
+    if (output_overlaps(so, B, H, Sq, D)) return fail("attn: o strides make output rows overlap");
     return 0;
 }
 
-Strides3 contiguous(int H, int S, int D) {
-    return Strides3{(long long)H * S * D, (long long)S * D, D};
+Strides contiguous(int H, int S, int D) {
+    return Strides{(long long)H * S * D, (long long)S * D, D, 1};
 }
 
 }  // namespace
@@ -928,13 +1051,13 @@ extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
                            const long long* q_strides, const long long* k_strides,
                            const long long* v_strides, const long long* o_strides) {
     g_err[0] = 0;
-    auto pick = [](const long long* p, Strides3 dflt) {
-        return p ? Strides3{p[0], p[1], p[2]} : dflt;
+    auto pick = [](const long long* p, Strides dflt) {
+        return p ? Strides{p[0], p[1], p[2], p[3]} : dflt;
     };
-    const Strides3 sq = pick(q_strides, contiguous(H, Sq, D));
-    const Strides3 sk = pick(k_strides, contiguous(H, Skv, D));
-    const Strides3 sv = pick(v_strides, contiguous(H, Skv, D));
-    const Strides3 so = pick(o_strides, contiguous(H, Sq, D));
+    const Strides sq = pick(q_strides, contiguous(H, Sq, D));
+    const Strides sk = pick(k_strides, contiguous(H, Skv, D));
+    const Strides sv = pick(v_strides, contiguous(H, Skv, D));
+    const Strides so = pick(o_strides, contiguous(H, Sq, D));
     if (check_args(q, k, v, o, B, H, Sq, Skv, D, dtype, sq, sk, sv, so)) return 1;
     if (B == 0 || H == 0 || Sq == 0) return 0;
     KArgs a;
@@ -955,8 +1078,9 @@ extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
     // finite score, i.e. the same uniform weights as c == 0.
     a.c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
     a.qsign = scale < 0.f ? -1.f : 1.f;
-    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, B * H, stream)
-                                                  : launch_t<f16>(a, B * H, stream);
+    const bool tl = token_contiguous(sk, sv, D);
+    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, B * H, tl, stream)
+                                                  : launch_t<f16>(a, B * H, tl, stream);
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;

@@ -39,15 +39,22 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o,
 
 /* attn_fwd() for fp16 or bf16 (dtype = ATTN_DTYPE_F16 / ATTN_DTYPE_BF16,
  * the same type for q, k, v and o) and strided tensors. Each *_strides
- * points to three element strides {batch, head, sequence} of that tensor,
- * or is NULL for the contiguous layout; the head dim is always contiguous.
- * q, k, v need 16-byte alignment and strides that are multiples of 8
- * elements, o 8-byte alignment and multiples of 4; k/v sequence strides
- * are at most 2^24; input strides may be 0 (a tensor broadcast over batch or
- * heads) but output rows must not overlap. Return codes as attn_fwd().
- * No counterpart in the reference, whose hook casts bf16 to fp16 and back
- * (deploy/gfx906_attention.py:71-75, 99-100) and whose binding copies
- * strided inputs (attn.cpp:15). */
+ * points to four element strides {batch, head, sequence, head dim} of that
+ * tensor, or is NULL for the contiguous layout. Strides are non-negative;
+ * input strides may be 0 (a tensor broadcast over batch or heads) but no two
+ * elements of o may share an address. Two layouts are accepted:
+ *  - head dim contiguous (stride 1) for q, k, v and o: q, k, v 16-byte
+ *    aligned with other strides multiples of 8 elements, o 8-byte aligned
+ *    with multiples of 4; k/v sequence strides at most 2^24;
+ *  - D == 512 with token-contiguous k and v (sequence stride 1, head-dim
+ *    stride not 1), as in a [b, c, h*w] activation viewed as
+ *    [b, 1, h*w, c]: k, v 16-byte aligned, batch/head/head-dim strides
+ *    multiples of 8, Skv % 8 == 0, (D-1)*stride_d + Skv < 2^30 per head;
+ *    q and o then take any strides (2-byte aligned).
+ * Return codes as attn_fwd(). No counterpart in the reference, whose hook
+ * casts bf16 to fp16 and back (deploy/gfx906_attention.py:71-75, 99-100) and
+ * whose binding copies strided inputs (attn.cpp:15), including the VAE's
+ * transposed views (deploy/gfx906_attention.py:102-104). */
 int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
                 int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream,
                 int dtype, const long long* q_strides, const long long* k_strides,

@@ -112,7 +112,9 @@ P = ctypes.c_void_p(0x10000)  # aligned, never dereferenced: every case below is
 
 def _ex(B=1, H=2, Sq=16, Skv=16, D=64, dtype=0, q=None, k=None, v=None, o=None, ptrs=None):
     lib = gfx906_amd.capi()
-    arr = [None if s is None else (ctypes.c_longlong * 3)(*s) for s in (q, k, v, o)]
+    # 3-tuples are {batch, head, seq} with a contiguous head dim
+    arr = [None if s is None else (ctypes.c_longlong * 4)(*s, *((1,) if len(s) == 3 else ()))
+           for s in (q, k, v, o)]
     pq, pk, pv, po = ptrs or (P, P, P, P)
     rc = lib.attn_fwd_ex(pq, pk, pv, po, B, H, Sq, Skv, D, 0.1, None, dtype, *arr)
     return rc, lib.attn_last_error()
@@ -218,3 +220,24 @@ def test_mfma_ceiling_library_rejects_bad_arguments_without_launch():
     for mode, iters, reps in ((3, 10, 1), (-1, 10, 1), (0, 0, 1), (0, 10, 0)):
         assert lib.mfma_ceiling(mode, iters, reps, ctypes.byref(tf), ctypes.byref(ghz)) == 1
     assert lib.mfma_ceiling(0, 10, 1, None, ctypes.byref(ghz)) == 1
+
+
+def test_ex_head_dim_stride_rules():
+    # outside D == 512 with token-contiguous k/v the head dim must be contiguous
+    rc, err = _ex(D=64, q=(2 * 16 * 64, 16 * 64, 1, 16))
+    assert rc == 1 and b"head dim must be contiguous" in err
+    rc, err = _ex(D=512, Skv=64, k=(2 * 64 * 512, 64 * 512, 512, 2))  # k d-strided, not token-contig
+    assert rc == 1 and b"head dim must be contiguous" in err
+    # token-contiguous k/v: Skv % 8, stride multiples, span
+    tk = (2 * 512 * 64, 512 * 64, 1, 64)
+    rc, err = _ex(D=512, Skv=63, k=(2 * 512 * 64, 512 * 64, 1, 64), v=(2 * 512 * 64, 512 * 64, 1, 64))
+    assert rc == 1 and b"Skv % 8" in err
+    rc, err = _ex(D=512, Skv=64, k=(2 * 512 * 64, 512 * 64, 1, 68), v=tk)
+    assert rc == 1 and b"multiples of 8" in err
+    rc, err = _ex(D=512, Skv=64, k=(0, 0, 1, 1 << 22), v=(0, 0, 1, 1 << 22))
+    assert rc == 1 and b"2^30" in err
+    rc, err = _ex(D=512, Skv=64, k=tk, v=tk, ptrs=(P, ctypes.c_void_p(0x10008), P, P))
+    assert rc == 1 and b"16-byte" in err
+    # ... with q and o of any strides, but o elements must not overlap
+    rc, err = _ex(D=512, Skv=64, k=tk, v=tk, o=(2 * 16 * 512, 16 * 512, 512, 0))
+    assert rc == 1 and b"overlap" in err

@@ -16,6 +16,7 @@ class FakeCuda:
     """Shape/dtype carrier that claims to live on a GPU."""
 
     is_cuda = True
+    device = torch.device("cpu")  # where the hook allocates its output in these tests
 
     def __init__(self, shape, dtype=torch.float16):
         self.shape = torch.Size(shape)
@@ -178,6 +179,33 @@ def test_vae_kernel_error_uses_selected_fallback():
     with mock.patch.object(loader, "load_attention", return_value=kernel):
         assert hooks.vae_attn(t, t, t, lambda q, k, v: "fallback") == "fallback"
     kernel.attn.assert_called_once()
+
+
+def test_vae_writes_nchw_output_in_place():
+    # q/k/v [b, c, h, w] -> token-contiguous [b, 1, h*w, c] views (sequence stride
+    # 1, channel stride h*w); the kernel writes a view of the returned tensor.
+    b, c, h, w = 2, 512, 3, 5
+    q, k, v = (torch.randn(b, c, h, w).half() for _ in range(3))
+    seen = {}
+
+    def fake_attn(qt, kt, vt, scale, out=None):
+        seen.update(q=qt, k=kt, scale=scale, out=out)
+        out.copy_(qt * 2)  # any function of the inputs, written through the view
+        return out
+
+    kernel = types.SimpleNamespace(attn=fake_attn)
+    with mock.patch.object(loader, "load_attention", return_value=kernel), \
+            mock.patch.object(torch.Tensor, "is_cuda", new_callable=mock.PropertyMock,
+                              return_value=True):
+        res = hooks.vae_attn(q, k, v, lambda *a: "fallback")
+    assert seen["scale"] == c ** -0.5
+    for name in ("q", "k", "out"):
+        t = seen[name]
+        assert t.shape == (b, 1, h * w, c) and t.stride(2) == 1 and t.stride(3) == h * w
+    assert seen["q"].data_ptr() == q.data_ptr()  # no copy of the input
+    assert res.shape == (b, c, h, w) and res.is_contiguous()
+    assert seen["out"].data_ptr() == res.data_ptr()
+    assert torch.equal(res, q * 2)
 
 
 def test_vae_ineligible_channels_use_fallback():
