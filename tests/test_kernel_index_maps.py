@@ -1,0 +1,168 @@
+"""CPU checks of two index maps the HIP kernels rely on, restated from the
+kernel source (the GPU parity tests check the kernels themselves):
+
+* the token-contiguous D = 512 attention tiles (attn_fwd_d512<T, true>): the
+  direct loads' chunk choice, the transposed K reads (ds_read_b64_tr_b16: in
+  each 16-lane group, lane i receives element i%4 of the 8 bytes read by lanes
+  4e + i/4, e = 0..3) and the V^T reads deliver exactly the MFMA operands, P's
+  key order matches V^T's, and no read pattern has LDS bank conflicts;
+* conv3d's incremental tap tracking (conv3d_mfma) agrees with the direct
+  division-based index for every k-tile and lane group.
+"""
+
+import numpy as np
+import pytest
+
+D, BN, ROWB = 512, 32, 64
+
+
+def tswz(r):
+    return (((r >> 2) & 1) << 1) | ((r >> 3) & 1)
+
+
+def tkey(kb, j, t):
+    return 8 * j + 4 * ((j + kb) & 1) + t
+
+
+def fill_tile(T):
+    """LDS image (uint16) of one K^T or V^T tile written by the direct loads:
+    lane l of 1 KB block blk (= wave + 8n) writes bytes blk*1024 + 16l, i.e.
+    row 16*blk + l/4, slot l%4, fetching key chunk tu = (l%4) ^ tswz(row)."""
+    lds = np.zeros(D * BN, dtype=np.uint16)
+    for blk in range(32):
+        for lane in range(64):
+            row = 16 * blk + lane // 4
+            tu = (lane & 3) ^ ((((lane >> 4) & 1) << 1) | ((lane >> 5) & 1))
+            assert tu == (lane & 3) ^ tswz(row)
+            base = blk * 1024 + lane * 16
+            assert base == row * ROWB + (lane & 3) * 16
+            lds[base // 2: base // 2 + 8] = T[row, 8 * tu: 8 * tu + 8]
+    return lds
+
+
+def ktr_addr(s, kb, g, h, i):
+    row = 32 * s + 8 * g + 4 * h + (i >> 2)
+    return row * ROWB + (((i & 3) ^ ((h << 1) | (g & 1))) * 16) + (((i & 3) + kb) & 1) * 8
+
+
+def vt_addr(ob, g, i):
+    return (16 * ob + i) * ROWB + ((g ^ tswz(i)) * 16)
+
+
+@pytest.fixture(scope="module")
+def tiles():
+    rng = np.random.default_rng(0)
+    K = rng.integers(0, 65535, size=(BN, D)).astype(np.uint16)  # [key][dim]
+    V = rng.integers(0, 65535, size=(BN, D)).astype(np.uint16)
+    return K, V, fill_tile(K.T.copy()), fill_tile(V.T.copy())
+
+
+def test_transposed_k_reads_give_the_qk_operand(tiles):
+    K, _, lk, _ = tiles
+    for s in range(16):
+        for kb in range(2):
+            for g in range(4):
+                reads = {(h, i): lk[ktr_addr(s, kb, g, h, i) // 2:][:4]
+                         for h in range(2) for i in range(16)}
+                for i in range(16):
+                    got = [reads[(h, 4 * e + i // 4)][i % 4] for h in range(2) for e in range(4)]
+                    key = tkey(kb, i >> 2, i & 3)
+                    want = [K[key, 32 * s + 8 * g + 4 * h + e] for h in range(2) for e in range(4)]
+                    assert got == want
+
+
+def test_vt_reads_match_p_key_order(tiles):
+    _, V, _, lv = tiles
+    for g in range(4):  # P after the odd-group swap holds keys 8g..8g+7 in order
+        b0 = [tkey(0, g, r) for r in range(4)]
+        b1 = [tkey(1, g, r) for r in range(4)]
+        assert (b1 + b0 if g & 1 else b0 + b1) == list(range(8 * g, 8 * g + 8))
+    for ob in range(32):
+        for g in range(4):
+            for i in range(16):
+                got = list(lv[vt_addr(ob, g, i) // 2:][:8])
+                assert got == [V[8 * g + e, 16 * ob + i] for e in range(8)]
+    keys = sorted(tkey(kb, j, t) for kb in range(2) for j in range(4) for t in range(4))
+    assert keys == list(range(BN))
+
+
+def conflict_free(addrs, nbytes):
+    banks = [(a // 4 + k) % 64 for a in addrs for k in range(nbytes // 4)]
+    return len(banks) == len(set(banks))
+
+
+def test_reads_are_bank_conflict_free():
+    for s in (0, 7):
+        for kb in range(2):
+            for h in range(2):
+                for half in range(2):  # 32 lanes served together
+                    addrs = [ktr_addr(s, kb, g, h, i) for g in (2 * half, 2 * half + 1)
+                             for i in range(16)]
+                    assert conflict_free(addrs, 8)
+    for ob in (0, 9):
+        for g in range(4):  # 16 lanes served together
+            assert conflict_free([vt_addr(ob, g, i) for i in range(16)], 16)
+
+
+def test_planted_swizzle_mistake_conflicts():
+    # The swizzle of the previous design ((row >> 2) & 3) with this key order
+    # puts both lane groups on the same halves.
+    addrs = []
+    for g in (0, 1):
+        for i in range(16):
+            row = 8 * g + (i >> 2)
+            addrs.append(row * ROWB + (((i & 3) ^ ((row >> 2) & 3)) * 16) + ((i & 3) & 1) * 8)
+    assert not conflict_free(addrs, 8)
+
+
+# -- conv3d taps -------------------------------------------------------------------------
+
+def tap_walk(C, T, R, S, xsd, xsh, xsw, kbr=32):
+    """Per lane group u: (gi, cc, toff) of every k-tile, as the kernel advances them."""
+    KG = C * T * R * S
+    nkt = -(-KG // kbr)
+    small = C < kbr
+    for u in range(4):
+        gi = 8 * u
+        tp = gi // C
+        cc, ts, tr = gi - tp * C, tp % S, (tp // S) % R
+        toff = (tp // (S * R)) * xsd + tr * xsh + ts * xsw
+        tstep = kbr // C if small else 0
+        cstep = kbr - tstep * C
+        dr, dt = xsh - S * xsw, xsd - R * xsh
+
+        def next_tap(go):
+            nonlocal ts, tr, toff
+            ts += go
+            toff += xsw if go else 0
+            ws = ts == S
+            ts = 0 if ws else ts
+            tr += ws
+            toff += dr if ws else 0
+            wr = tr == R
+            tr = 0 if wr else tr
+            toff += dt if wr else 0
+
+        for _ in range(-(-nkt // 4) * 4):
+            yield gi, cc, toff, KG
+            gi += kbr
+            if small:
+                for i in range(4):
+                    next_tap(i < tstep)
+            cc += cstep
+            wrap = cc >= C
+            cc -= C if wrap else 0
+            next_tap(wrap)
+
+
+@pytest.mark.parametrize("C", [8, 16, 24, 32, 40, 64, 96, 512])
+@pytest.mark.parametrize("trs", [(1, 1, 1), (3, 3, 3), (1, 3, 3), (2, 3, 2), (5, 2, 3)])
+def test_conv3d_tap_tracking_matches_division(C, trs):
+    T, R, S = trs
+    xsd, xsh, xsw = 7919 * C, 131 * C, C
+    for gi, cc, toff, KG in tap_walk(C, T, R, S, xsd, xsh, xsw):
+        if gi >= KG:
+            continue
+        tp = gi // C
+        t, r, s = tp // (R * S), (tp // S) % R, tp % S
+        assert (cc, toff) == (gi % C, t * xsd + r * xsh + s * xsw)
