@@ -113,8 +113,8 @@ def vae_attn(q, k, v, fallback):
     b, c, h, w = q.shape
 
     def tokens(x):  # [b, c, h, w] -> [b, 1, h*w, c]: a token-contiguous view (sequence
-        # stride 1, channel stride h*w); the op transposes it (faster on gfx950 than
-        # the in-place kernel) and fills the [b, c, h, w] output through its view
+        # stride 1, channel stride h*w); the op reads and writes such views in place,
+        # or through copies where that is faster (h*w > 8192)
         return x.reshape(b, c, h * w).transpose(1, 2).unsqueeze(1)
 
     out = torch.empty((b, c, h, w), dtype=q.dtype, device=q.device)

@@ -8,6 +8,10 @@
 // returns without synchronising.
 //
 // Beyond the reference binding:
+//  * Problems whose workgroups leave CUs idle (one head of a VAE, short
+//    sequences) split the key range over more workgroups and merge the
+//    partial results (attn_fwd_split), with a workspace from torch's
+//    allocator; results then agree with the unsplit kernel to fp32 rounding.
 //  * bf16 q/k/v run natively (bf16 MFMA), with a bf16 output; the reference
 //    accepts fp16 only and its hook casts bf16 around it
 //    (deploy/gfx906_attention.py:71-75).
@@ -15,18 +19,20 @@
 //    the other strides are multiples of 8 elements (16-byte aligned data);
 //    only other layouts are copied, where the reference always calls
 //    .contiguous() (attn.cpp:15). The VAE's token-contiguous views
-//    ([b, c, h*w] seen as [b, 1, h*w, c], deploy/gfx906_attention.py:102-104)
-//    are copied too, on purpose: the kernel that reads them in place
-//    (attn_fwd_ex with their strides) needs transposing LDS reads for K and
-//    is slower on gfx950 than a transpose copy plus the contiguous kernel
-//    (1.42 against 1.18 ms at h*w = 16384).
+//    ([b, c, h*w] seen as [b, 1, h*w, c], deploy/gfx906_attention.py:102-104,
+//    D = 512) are read in place, q and out with them, up to Skv = 8192; past
+//    that they are copied, on purpose: the in-place kernel needs transposing
+//    LDS reads for K, a cost that grows with Skv^2 while the copies grow with
+//    Skv (measured on MI355X with split key ranges: in place 0.102 against
+//    0.124 ms copied at h*w = 4096, 0.91 against 0.76 ms at 16384).
 //  * `out`, if given, is written instead of allocating: any [B, H, Sq, D]
 //    view of q's dtype and device whose elements do not overlap, e.g. the
-//    transpose of a [B, Sq, H, D] buffer; a view with a strided head dim
-//    (the VAE's [b, 1, h*w, c] view of a [b, c, h, w] output) is filled
-//    through a contiguous temporary. It must not overlap k or v (every
-//    workgroup of a head reads them); it may be q itself (a workgroup reads
-//    its own query rows before writing them).
+//    transpose of a [B, Sq, H, D] buffer or the VAE's [b, 1, h*w, c] view of
+//    a [b, c, h, w] output (written in place with the token-contiguous
+//    kernel, else through a contiguous temporary when its head dim is
+//    strided). It must not overlap k or v (every workgroup of a head reads
+//    them); it may be q itself (a workgroup reads its own query rows before
+//    writing them).
 //  * Checks raising RuntimeError: k and v must match q's dtype and device,
 //    sizes must fit the kernel's indexing, and a launch error is reported
 //    instead of being dropped.
@@ -59,6 +65,22 @@ bool readable_in_place(const torch::Tensor& t, bool kv) {
         if (s[d] < 0 || s[d] % 8) return false;
     return !kv || s[2] <= (1 << 24);
 }
+
+// Whether k (or v) is in the token-contiguous D = 512 layout the kernel
+// reads in place: sequence stride 1, head-dim stride a multiple of 8 other
+// than 1, batch/head strides multiples of 8, 16-byte aligned data, Skv % 8 ==
+// 0 and a per-head span below 2^30 elements.
+bool token_contiguous_kv(const torch::Tensor& t) {
+    const int64_t D = t.size(3), S = t.size(2);
+    const auto s = strides4(t);
+    if (D != 512 || S % 8 || t.stride(2) != 1 || s[3] == 1 || s[3] % 8) return false;
+    if (s[0] % 8 || s[1] % 8 || reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) return false;
+    return (D - 1) * s[3] + S < (int64_t(1) << 30);
+}
+
+// Largest Skv for which reading token-contiguous k/v in place beats copying
+// them (see the file comment).
+constexpr int64_t kInPlaceMaxSkv = 8192;
 
 torch::Tensor as_input(const torch::Tensor& t, bool kv) {
     return readable_in_place(t, kv) ? t : t.clone(at::MemoryFormat::Contiguous);
@@ -97,19 +119,29 @@ torch::Tensor attn(torch::Tensor q, torch::Tensor k, torch::Tensor v, double sca
         o = torch::empty({B, H, Sq, D}, q.options().memory_format(at::MemoryFormat::Contiguous));
     }
     if (o.numel() == 0) return o;
-    // The head dim of every tensor the kernel touches is contiguous: inputs
-    // are copied and out staged as needed.
-    const auto qi = as_input(q, false), ki = as_input(k, true), vi = as_input(v, true);
-    const bool staged = o.stride(3) != 1;
+    // Token-contiguous k and v (D = 512, Skv <= kInPlaceMaxSkv): read in
+    // place, q and out with any strides. Otherwise the head dim of every
+    // tensor the kernel touches is contiguous: inputs are copied and out
+    // staged as needed.
+    const bool tl = Skv <= kInPlaceMaxSkv && token_contiguous_kv(k) && token_contiguous_kv(v);
+    const auto qi = tl ? q : as_input(q, false);
+    const auto ki = tl ? k : as_input(k, true), vi = tl ? v : as_input(v, true);
+    const bool staged = !tl && o.stride(3) != 1;
     torch::Tensor oo =
         staged ? torch::empty({B, H, Sq, D}, q.options().memory_format(at::MemoryFormat::Contiguous))
                : o;
     const auto sq = strides4(qi), sk = strides4(ki), sv = strides4(vi), so = strides4(oo);
     const int dtype = q.dtype() == torch::kBFloat16 ? ATTN_DTYPE_BF16 : ATTN_DTYPE_F16;
-    const int rc = attn_fwd_ex(qi.data_ptr(), ki.data_ptr(), vi.data_ptr(), oo.data_ptr(), (int)B,
-                               (int)H, (int)Sq, (int)Skv, (int)D, (float)scale,
-                               c10::hip::getCurrentHIPStream().stream(), dtype, sq.data(),
-                               sk.data(), sv.data(), so.data());
+    // Problems too small to fill the GPU split the key range; the partial
+    // results go to a workspace from torch's caching allocator.
+    const size_t ws_bytes = attn_split_workspace_bytes((int)B, (int)H, (int)Sq, (int)Skv, (int)D);
+    torch::Tensor ws;
+    if (ws_bytes) ws = torch::empty({(int64_t)ws_bytes}, q.options().dtype(torch::kUInt8));
+    const int rc = attn_fwd_split(qi.data_ptr(), ki.data_ptr(), vi.data_ptr(), oo.data_ptr(), (int)B,
+                                  (int)H, (int)Sq, (int)Skv, (int)D, (float)scale,
+                                  c10::hip::getCurrentHIPStream().stream(), dtype, sq.data(),
+                                  sk.data(), sv.data(), so.data(),
+                                  ws_bytes ? ws.data_ptr() : nullptr, ws_bytes);
     TORCH_CHECK(rc == 0, "kernel: ", attn_last_error() ? attn_last_error() : "launch failed");
     if (staged) o.copy_(oo);
     return o;

@@ -44,6 +44,7 @@
 #include <stdint.h>
 #include <math.h>
 #include <type_traits>
+#include <algorithm>
 
 #include "gfx906_amd_attn.h"
 
@@ -92,6 +93,13 @@ struct KArgs {
     Strides sq, sk, sv, so;
     int H, Sq, Skv, D;
     float c, qsign;
+    // Split key range (kernels instantiated with SPLIT): workgroup split s of
+    // nsplit takes keys [s*split_len, (s+1)*split_len) and writes its
+    // unnormalised O (fp32) to ws_o[s][bh][row][0..D) and its (m, l) to
+    // ws_ml[s][bh][row][0..1]; attn_combine merges them.
+    int BH, nsplit, split_len;
+    float* ws_o;
+    float* ws_ml;
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -330,9 +338,10 @@ __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int 
 }
 #endif
 
-// grid: ceil(Sq / BM) * B*H workgroups, query tiles of one head adjacent;
-// block: NW*64 threads.
-template <class C, bool PAD, class T>
+// grid: ceil(Sq / BM) * B*H (* nsplit with SPLIT) workgroups, query tiles of
+// one head adjacent (the splits of one query tile adjacent); block: NW*64
+// threads.
+template <class C, bool PAD, class T, bool SPLIT>
 __global__ void __launch_bounds__(C::NT, C::OCC)
 attn_fwd_pipe(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -349,19 +358,27 @@ attn_fwd_pipe(const KArgs a) {
     __shared__ __attribute__((aligned(1024))) char st2[C::STAGE];
     __shared__ __attribute__((aligned(1024))) char st3[C::STAGE];
 
-    const int Sq = a.Sq, Skv = a.Skv, D = a.D;
+    const int Sq = a.Sq, D = a.D;
     const float c = a.c;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, r32 = lane & 31;
     const int j16 = lane & 15, G = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    const int bh = blockIdx.x / nqt;
-    const int qt = blockIdx.x % nqt;
+    int wg = blockIdx.x, split = 0;
+    if constexpr (SPLIT) {
+        split = wg % a.nsplit;
+        wg /= a.nsplit;
+    }
+    const int bh = wg / nqt;
+    const int qt = wg % nqt;
     const int b = bh / a.H, h = bh - b * a.H;
+    // This workgroup's keys: [kv0, kv0 + Skv) of the head.
+    const int kv0 = SPLIT ? split * a.split_len : 0;
+    const int Skv = SPLIT ? max(0, min(a.Skv - kv0, a.split_len)) : a.Skv;
     const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
-    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h;
-    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h + kv0 * a.sk.s;
+    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h + kv0 * a.sv.s;
     T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
     const int qrow0 = qt * C::BM + wave * 32 * QB + r32;  // this lane's rows: qrow0 + 32 qb
     const int ntiles = (Skv + C::BN - 1) / C::BN;
@@ -542,6 +559,29 @@ attn_fwd_pipe(const KArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
     }
 
+    if constexpr (SPLIT) {  // unnormalised O and (m, l) of this key range
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const int row = qrow0 + 32 * qb;
+            const float l = half_swap_sum(l_run[qb]);
+            if (row < Sq) {
+                const long long r = ((long long)split * a.BH + bh) * Sq + row;
+                float* wo = a.ws_o + r * D;
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int d0 = 32 * ob + 8 * rr + 4 * g;
+                        if (!PAD || d0 < D)
+                            *reinterpret_cast<f32x4*>(wo + d0) =
+                                f32x4{oacc[qb][ob][4 * rr], oacc[qb][ob][4 * rr + 1],
+                                      oacc[qb][ob][4 * rr + 2], oacc[qb][ob][4 * rr + 3]};
+                    }
+                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[qb], l};
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int row = qrow0 + 32 * qb;
@@ -652,7 +692,7 @@ __device__ __attribute__((noinline)) Rescale512<T> d512_rescale(f32x4 S0, f32x4 
 // grid: ceil(Sq / 128) * B*H workgroups; block: 512 threads. TL: k and v in
 // the token-contiguous layout (Cfg512T), q and o read and written element by
 // element with any strides.
-template <class T, bool TL>
+template <class T, bool TL, bool SPLIT>
 __global__ void __launch_bounds__(Cfg512::NT, 1)
 attn_fwd_d512(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -667,18 +707,26 @@ attn_fwd_d512(const KArgs a) {
     constexpr int VOFF = TL ? Cfg512T::TILE : C::KTILE;  // V (V^T) tile within a stage
     __shared__ __attribute__((aligned(1024))) char lds[TL ? Cfg512T::LDS : C::LDS];  // 2 x (K, V)
 
-    const int Sq = a.Sq, Skv = a.Skv;
+    const int Sq = a.Sq;
     const float c = a.c;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    const int bh = blockIdx.x / nqt;
-    const int qt = blockIdx.x % nqt;
+    int wg = blockIdx.x, split = 0;
+    if constexpr (SPLIT) {
+        split = wg % a.nsplit;
+        wg /= a.nsplit;
+    }
+    const int bh = wg / nqt;
+    const int qt = wg % nqt;
     const int b = bh / a.H, h = bh - b * a.H;
+    // This workgroup's keys: [kv0, kv0 + Skv) of the head.
+    const int kv0 = SPLIT ? split * a.split_len : 0;
+    const int Skv = SPLIT ? max(0, min(a.Skv - kv0, a.split_len)) : a.Skv;
     const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
-    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h;
-    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h + kv0 * a.sk.s;
+    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h + kv0 * a.sv.s;
     T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
     const long long kss = a.sk.s, vss = a.sv.s;
     const int qrow = qt * C::BM + wave * 16 + i;
@@ -895,6 +943,16 @@ attn_fwd_d512(const KArgs a) {
     }
 
     const float l = quad_group_sum(l_run);
+    if constexpr (SPLIT) {  // unnormalised O and (m, l) of this key range
+        if (live) {
+            const long long r = ((long long)split * a.BH + bh) * Sq + qrow;
+            float* wo = a.ws_o + r * D;
+#pragma unroll
+            for (int ob = 0; ob < NOB; ++ob) *reinterpret_cast<f32x4*>(wo + 16 * ob + 4 * g) = oacc[ob];
+            if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run, l};
+        }
+        return;
+    }
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (live) {
         T* op = Oh + qrow * a.so.s;
@@ -916,6 +974,55 @@ attn_fwd_d512(const KArgs a) {
 #endif
 }
 
+// Merge of the split key ranges: per output row, with m* the largest
+// running max of its splits and w_s = exp2(m_s - m*),
+//     o = sum_s w_s O_s / sum_s w_s l_s
+// rounded to the element type. One thread per row and 4 consecutive dims.
+struct CombArgs {
+    const float* ws_o;
+    const float* ws_ml;
+    void* o;
+    Strides so;
+    int H, Sq, D, BH, nsplit;
+};
+
+template <class T>
+__global__ void __launch_bounds__(256) attn_combine(const CombArgs c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using E = Elem<T>;
+    const int dq = c.D / 4;
+    const long long rows = (long long)c.BH * c.Sq;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * dq) return;
+    const long long row = idx / dq;
+    const int d0 = (int)(idx - row * dq) * 4;
+    float mx = -3.0e38f;
+    for (int s = 0; s < c.nsplit; ++s) mx = fmaxf(mx, c.ws_ml[2 * (s * rows + row)]);
+    f32x4 acc = {};
+    float l = 0.f;
+    for (int s = 0; s < c.nsplit; ++s) {
+        const long long r = s * rows + row;
+        const float w = __builtin_amdgcn_exp2f(c.ws_ml[2 * r] - mx);
+        acc += w * *reinterpret_cast<const f32x4*>(c.ws_o + r * c.D + d0);
+        l += w * c.ws_ml[2 * r + 1];
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const auto h0 = E::cvt2(acc[0] * inv, acc[1] * inv);
+    const auto h1 = E::cvt2(acc[2] * inv, acc[3] * inv);
+    const int bh = (int)(row / c.Sq), srow = (int)(row - (long long)bh * c.Sq);
+    const int b = bh / c.H, h = bh - b * c.H;
+    T* op = (T*)c.o + b * c.so.b + h * c.so.h + srow * c.so.s + d0 * c.so.d;
+    if (c.so.d == 1 && (reinterpret_cast<uintptr_t>(op) & 7) == 0) {
+        *reinterpret_cast<typename E::x4*>(op) = typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+    } else {
+        op[0] = h0[0];
+        op[c.so.d] = h0[1];
+        op[2 * c.so.d] = h1[0];
+        op[3 * c.so.d] = h1[1];
+    }
+#endif
+}
+
 thread_local char g_err[256];
 
 void set_err(const char* msg) {
@@ -927,26 +1034,88 @@ void set_err(const char* msg) {
 using Cfg128 = Cfg<128, 8, 1, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
 using Cfg64 = Cfg<64, 8, 1, 2>;    // 64 KB: two workgroups, four waves per SIMD
 
-template <class T>
-hipError_t launch_t(const KArgs& a, int BH, bool tl, hipStream_t s) {
+template <class T, bool SPLIT>
+void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
     const int D = a.D;
     if (D == 512) {
-        dim3 grid((unsigned)((a.Sq + Cfg512::BM - 1) / Cfg512::BM) * (unsigned)BH);
+        dim3 grid((unsigned)((a.Sq + Cfg512::BM - 1) / Cfg512::BM) * nwg);
         if (tl)
-            hipLaunchKernelGGL((attn_fwd_d512<T, true>), grid, dim3(Cfg512::NT), 0, s, a);
+            hipLaunchKernelGGL((attn_fwd_d512<T, true, SPLIT>), grid, dim3(Cfg512::NT), 0, s, a);
         else
-            hipLaunchKernelGGL((attn_fwd_d512<T, false>), grid, dim3(Cfg512::NT), 0, s, a);
+            hipLaunchKernelGGL((attn_fwd_d512<T, false, SPLIT>), grid, dim3(Cfg512::NT), 0, s, a);
     } else if (D == 128) {
-        dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * (unsigned)BH);
-        hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T>), grid, dim3(Cfg128::NT), 0, s, a);
+        dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * nwg);
+        hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T, SPLIT>), grid, dim3(Cfg128::NT), 0, s, a);
     } else {
-        dim3 grid((unsigned)((a.Sq + Cfg64::BM - 1) / Cfg64::BM) * (unsigned)BH);
+        dim3 grid((unsigned)((a.Sq + Cfg64::BM - 1) / Cfg64::BM) * nwg);
         if (D == 64)
-            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T>), grid, dim3(Cfg64::NT), 0, s, a);
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T, SPLIT>), grid, dim3(Cfg64::NT), 0, s, a);
         else
-            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T>), grid, dim3(Cfg64::NT), 0, s, a);
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T, SPLIT>), grid, dim3(Cfg64::NT), 0, s, a);
     }
+}
+
+// Launches the kernel for the whole problem, or (a.nsplit > 1) its split
+// key ranges and the merge.
+template <class T>
+hipError_t launch_t(const KArgs& a, bool tl, hipStream_t s) {
+    if (a.nsplit <= 1) {
+        launch_kernel<T, false>(a, (unsigned)a.BH, tl, s);
+        return hipGetLastError();
+    }
+    launch_kernel<T, true>(a, (unsigned)a.BH * (unsigned)a.nsplit, tl, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    CombArgs c;
+    c.ws_o = a.ws_o;
+    c.ws_ml = a.ws_ml;
+    c.o = a.o;
+    c.so = a.so;
+    c.H = a.H;
+    c.Sq = a.Sq;
+    c.D = a.D;
+    c.BH = a.BH;
+    c.nsplit = a.nsplit;
+    const long long threads = (long long)a.BH * a.Sq * (a.D / 4);
+    hipLaunchKernelGGL((attn_combine<T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       c);
     return hipGetLastError();
+}
+
+// Number of CUs of the current device.
+int cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
+// Split of the key range for problems whose grid leaves CUs idle: enough
+// splits to give every workgroup slot (one per CU for D = 128 and 512, two
+// for D <= 64) a workgroup, with at least four key tiles per split.
+struct SplitPlan {
+    int nsplit, split_len;
+};
+SplitPlan plan_split(int B, int H, int Sq, int Skv, int D) {
+    const int bm = D == 512 ? Cfg512::BM : (D == 128 ? Cfg128::BM : Cfg64::BM);
+    const int bn = D == 512 ? Cfg512::BN : Cfg128::BN;
+    const int per_cu = D == 512 || D == 128 ? 1 : 2;
+    const long long units = (long long)B * H * ((Sq + bm - 1) / bm);
+    const long long slots = (long long)cu_count() * per_cu;
+    if (Skv == 0 || units == 0 || units >= slots) return {1, 0};
+    const int tiles = (Skv + bn - 1) / bn;
+    int ns = (int)std::min<long long>((slots + units - 1) / units, tiles / 4);
+    if (ns <= 1) return {1, 0};
+    const int per = (tiles + ns - 1) / ns;  // tiles per split
+    ns = (tiles + per - 1) / per;           // no empty splits
+    return {ns, per * bn};
+}
+
+size_t split_ws_bytes(const SplitPlan& p, int B, int H, int Sq, int D) {
+    if (p.nsplit <= 1) return 0;
+    const size_t rows = (size_t)p.nsplit * B * H * Sq;
+    return rows * D * 4 + rows * 2 * 4 + 16;
 }
 
 // Whether two elements of an output tensor can share an address: the
@@ -1046,10 +1215,14 @@ Strides contiguous(int H, int S, int D) {
 
 extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr; }
 
-extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o, int B, int H,
-                           int Sq, int Skv, int D, float scale, hipStream_t stream, int dtype,
-                           const long long* q_strides, const long long* k_strides,
-                           const long long* v_strides, const long long* o_strides) {
+namespace {
+
+// attn_fwd_ex (workspace_bytes == SIZE_MAX: never split) and attn_fwd_split.
+int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
+                  int Skv, int D, float scale, hipStream_t stream, int dtype,
+                  const long long* q_strides, const long long* k_strides,
+                  const long long* v_strides, const long long* o_strides, void* workspace,
+                  size_t workspace_bytes) {
     g_err[0] = 0;
     auto pick = [](const long long* p, Strides dflt) {
         return p ? Strides{p[0], p[1], p[2], p[3]} : dflt;
@@ -1078,14 +1251,61 @@ extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
     // finite score, i.e. the same uniform weights as c == 0.
     a.c = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
     a.qsign = scale < 0.f ? -1.f : 1.f;
+    a.BH = B * H;
+    a.nsplit = 1;
+    a.split_len = 0;
+    a.ws_o = nullptr;
+    a.ws_ml = nullptr;
+    if (workspace_bytes != (size_t)-1) {  // attn_fwd_split: split the keys if it pays
+        const SplitPlan p = plan_split(B, H, Sq, Skv, D);
+        const size_t need = split_ws_bytes(p, B, H, Sq, D);
+        if (need) {
+            if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16) {
+                set_err("attn: workspace missing, misaligned or smaller than "
+                        "attn_split_workspace_bytes()");
+                return 1;
+            }
+            a.nsplit = p.nsplit;
+            a.split_len = p.split_len;
+            a.ws_o = (float*)workspace;
+            a.ws_ml = a.ws_o + (size_t)p.nsplit * B * H * Sq * D;
+        }
+    }
     const bool tl = token_contiguous(sk, sv, D);
-    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, B * H, tl, stream)
-                                                  : launch_t<f16>(a, B * H, tl, stream);
+    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, tl, stream)
+                                                  : launch_t<f16>(a, tl, stream);
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;
     }
     return 0;
+}
+
+}  // namespace
+
+extern "C" int attn_fwd_ex(const void* q, const void* k, const void* v, void* o, int B, int H,
+                           int Sq, int Skv, int D, float scale, hipStream_t stream, int dtype,
+                           const long long* q_strides, const long long* k_strides,
+                           const long long* v_strides, const long long* o_strides) {
+    return attn_fwd_impl(q, k, v, o, B, H, Sq, Skv, D, scale, stream, dtype, q_strides, k_strides,
+                         v_strides, o_strides, nullptr, (size_t)-1);
+}
+
+extern "C" size_t attn_split_workspace_bytes(int B, int H, int Sq, int Skv, int D) {
+    if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 ||
+        !((D <= 64 && D > 0 && D % 8 == 0) || D == 128 || D == 512))
+        return 0;
+    return split_ws_bytes(plan_split(B, H, Sq, Skv, D), B, H, Sq, D);
+}
+
+extern "C" int attn_fwd_split(const void* q, const void* k, const void* v, void* o, int B, int H,
+                              int Sq, int Skv, int D, float scale, hipStream_t stream, int dtype,
+                              const long long* q_strides, const long long* k_strides,
+                              const long long* v_strides, const long long* o_strides,
+                              void* workspace, size_t workspace_bytes) {
+    if (workspace_bytes == (size_t)-1) workspace_bytes -= 1;
+    return attn_fwd_impl(q, k, v, o, B, H, Sq, Skv, D, scale, stream, dtype, q_strides, k_strides,
+                         v_strides, o_strides, workspace, workspace_bytes);
 }
 
 extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,

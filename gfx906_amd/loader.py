@@ -67,6 +67,10 @@ def capi() -> ctypes.CDLL:
     strides = ctypes.POINTER(ctypes.c_longlong)
     lib.attn_fwd_ex.argtypes = args + [ctypes.c_int] + [strides] * 4
     lib.attn_fwd_ex.restype = ctypes.c_int
+    lib.attn_fwd_split.argtypes = lib.attn_fwd_ex.argtypes + [ctypes.c_void_p, ctypes.c_size_t]
+    lib.attn_fwd_split.restype = ctypes.c_int
+    lib.attn_split_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.attn_split_workspace_bytes.restype = ctypes.c_size_t
     lib.attn_last_error.argtypes = []
     lib.attn_last_error.restype = ctypes.c_char_p
     return lib

@@ -13,6 +13,7 @@
 #ifndef GFX906_AMD_ATTN_H
 #define GFX906_AMD_ATTN_H
 
+#include <stddef.h>
 #include <hip/hip_runtime_api.h>
 
 #ifdef __cplusplus
@@ -60,8 +61,29 @@ int attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
                 int dtype, const long long* q_strides, const long long* k_strides,
                 const long long* v_strides, const long long* o_strides);
 
-/* Message for the last failed launch()/attn_fwd()/attn_fwd_ex() on the
- * calling thread, or NULL if the last call succeeded. No counterpart in the
+/* Bytes of device workspace attn_fwd_split() needs for this problem on the
+ * current device: 0 when the problem's workgroups already fill the GPU (the
+ * call then runs as attn_fwd_ex()), else room for the partial results of the
+ * split key ranges. No counterpart in the reference. */
+size_t attn_split_workspace_bytes(int B, int H, int Sq, int Skv, int D);
+
+/* attn_fwd_ex() that, when B*H*Sq is too small to fill the GPU (a VAE
+ * attention over one head, short problems), splits the key range over more
+ * workgroups: each writes its unnormalised partial output and running
+ * max/sum to `workspace` (device memory, 16-byte aligned, at least
+ * attn_split_workspace_bytes() bytes; may be NULL when that is 0) and a
+ * second kernel merges them into o. Same arguments and return codes as
+ * attn_fwd_ex(), plus 1 for a missing or short workspace. Results agree with
+ * attn_fwd_ex() to fp32 rounding of the merge (not bit for bit). Calls on one
+ * workspace must not overlap. No counterpart in the reference. */
+int attn_fwd_split(const void* q, const void* k, const void* v, void* o,
+                   int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream,
+                   int dtype, const long long* q_strides, const long long* k_strides,
+                   const long long* v_strides, const long long* o_strides,
+                   void* workspace, size_t workspace_bytes);
+
+/* Message for the last failed launch()/attn_fwd()/attn_fwd_ex()/
+ * attn_fwd_split() on the calling thread, or NULL if the last call succeeded. No counterpart in the
  * reference, whose launch() (attn_kernel.hip:710-742) never reports errors. */
 const char* attn_last_error(void);
 

@@ -241,3 +241,26 @@ def test_ex_head_dim_stride_rules():
     # ... with q and o of any strides, but o elements must not overlap
     rc, err = _ex(D=512, Skv=64, k=tk, v=tk, o=(2 * 16 * 512, 16 * 512, 512, 0))
     assert rc == 1 and b"overlap" in err
+
+
+# -- attn_fwd_split: workspace sizing and rejections (no GPU: plans assume 256 CUs) ------
+
+def test_split_workspace_bytes():
+    lib = gfx906_amd.capi()
+    assert lib.attn_split_workspace_bytes(1, 16, 16384, 16384, 128) == 0   # fills the GPU
+    assert lib.attn_split_workspace_bytes(1, 4, 8192, 8192, 512) == 0      # c4: 256 workgroups
+    # VAE 64x64: 32 query tiles of 128 rows; 8 splits of 512 keys
+    assert lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 512) == 8 * 4096 * (512 + 2) * 4 + 16
+    # too few key tiles to split (fewer than 8 = 2 splits x 4 tiles)
+    assert lib.attn_split_workspace_bytes(1, 1, 300, 400, 128) == 0
+    for bad in ((0, 1, 8, 8, 64), (1, 1, 8, 0, 64), (1, 1, 8, 8, 96)):
+        assert lib.attn_split_workspace_bytes(*bad) == 0
+
+
+def test_split_rejects_missing_or_short_workspace():
+    lib = gfx906_amd.capi()
+    need = lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 512)
+    for ws, nbytes in ((None, need), (P, need - 16), (ctypes.c_void_p(0x10008), need)):
+        rc = lib.attn_fwd_split(P, P, P, P, 1, 1, 4096, 4096, 512, 0.04, None, 0,
+                                None, None, None, None, ws, nbytes)
+        assert rc == 1 and b"workspace" in lib.attn_last_error()
