@@ -70,9 +70,9 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy rescale: a block whose lane row sum exceeds this takes the exact max.
 constexpr float kLsumLimit = 32768.0f;
-// Lazy-rescale threshold of the D = 512 kernel in log2 units: p <= 2^kTau.
-constexpr float kTau = 8.0f;
-constexpr float kPmaxLimit = 256.0f;  // 2^kTau
+// Lazy-rescale threshold of the D = 512 kernel: a tile whose largest p
+// exceeds 2^8 takes the exact max.
+constexpr float kPmaxLimit = 256.0f;
 // sched_group_barrier instruction classes
 constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
 
@@ -655,7 +655,8 @@ __host__ __device__ constexpr int tkey(int kb, int j, int t) { return 8 * j + 4 
 
 #if defined(__HIP_DEVICE_COMPILE__)
 // Rare path of the D = 512 kernel: the tile's scores exceed the running max by
-// more than kTau. Returns the new max, the rescale factor for O and l, and P
+// more than 8 (log2 units, p > kPmaxLimit). Returns the new max, the rescale
+// factor for O and l, and P
 // and the tile's row sum recomputed with the new max. Kept out of line (and
 // away from O, which stays in registers) so the hot loop does not reserve
 // registers for it.
