@@ -12,20 +12,23 @@
 //    the A operand of v_mfma_f32_32x32x16_f16, a lane's accumulator holds
 //    four runs of four consecutive output channels of one voxel: the
 //    channels-innermost output, bias and residual move as 8-byte vectors.
-//  * Tiles of 128 channels x 64*NB voxels x 32 reduction elements (NB = 2, 3
-//    or 4, chosen per problem for how the tile count fills the CUs), 4 waves
-//    of 64 x 32*NB (2 x NB MFMA blocks), two workgroups per CU whose
-//    barriers are independent. Both operand tiles go from HBM into LDS with
-//    buffer loads to LDS (no VGPR staging); the input gather uses a per-lane
-//    offset (voxel base + the offset of the lane's tap, advanced
-//    incrementally from k-tile to k-tile), and lanes past M, K or the
-//    reduction length get an out-of-range offset, so the load returns zeros.
-//    LDS rows are 64 bytes with 16-byte units XOR-swizzled; a ring of three
-//    or four stages keeps the loads of the next k-tiles in flight, k-tiles
-//    past the end load zeros (so every wait count is static), and the
-//    barrier waits for this wave's LDS reads only, not for loads in flight.
+//  * Tiles of 128 channels x 64*NB voxels x KB reduction elements (NB = 2, 3
+//    or 4 and KB = 32 or 64, chosen per problem for how the tile count fills
+//    the CUs and how long the reduction is), 4 waves of 64 x 32*NB (2 x NB
+//    MFMA blocks), two workgroups per CU whose barriers are independent.
+//    Both operand tiles go from HBM into LDS with buffer loads to LDS (no
+//    VGPR staging); the input gather uses a per-lane offset (voxel base +
+//    the offset of the lane's tap, advanced incrementally from k-tile to
+//    k-tile), and lanes past M, K or the reduction length get an
+//    out-of-range offset, so the load returns zeros. LDS rows are 2*KB bytes
+//    (with KB = 64 each row is one whole 128-byte line of a weight row or of
+//    a voxel's channels) with 16-byte units XOR-swizzled; a ring of two to
+//    four stages keeps the loads of the next k-tiles in flight, k-tiles past
+//    the end load zeros (so every wait count is static), and the barrier
+//    waits for this wave's LDS reads only, not for loads in flight.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
 
 #include "gfx906_amd_conv3d.h"
@@ -52,30 +55,40 @@ struct ConvArgs {
 };
 
 constexpr int kBCh = 128;              // output channels per workgroup (GEMM rows)
-constexpr int kBR = 32;                // reduction elements per k-tile
 constexpr int kNT = 256;               // 4 waves: 2 along channels x 2 along voxels
-constexpr int kRowB = kBR * 2;         // bytes per LDS row: 4 units of 16 bytes
-constexpr int kWTile = kBCh * kRowB;   // 8 KB: one W tile
 constexpr int kMaxTaps = 1024;
 constexpr unsigned kOOB = 0xFFFFFFF0u;  // buffer offset past any range: loads zeros
 
 // Per-configuration sizes: NB 32-voxel MFMA blocks per wave (64*NB voxels per
-// workgroup), NST stages in the LDS ring.
-template <int NB, int NST>
+// workgroup), NST stages in the LDS ring, KB reduction elements per k-tile
+// (LDS rows of 2*KB bytes: 32 -> 64-byte rows, 64 -> 128-byte rows, so that
+// each row of a tile is one whole 128-byte line of the weights or of a voxel).
+template <int NB, int NST, int KB>
 struct ConvCfg {
-    static constexpr int BVX = 64 * NB;            // output voxels per workgroup
-    static constexpr int XTILE = BVX * kRowB;      // bytes of one X tile
-    static constexpr int STAGE = kWTile + XTILE;   // W tile, then X tile
-    static constexpr int LOADS = 2 + NB;           // 1 KB loads per wave per k-tile
-    static constexpr int OCC = 2;                  // workgroups per CU
+    static constexpr int ROWB = 2 * KB;             // bytes per LDS row
+    static constexpr int UNITS = ROWB / 16;         // 16-byte units per row
+    static constexpr int RPB = 1024 / ROWB;         // rows per 1 KB load block
+    static constexpr int KSTEPS = KB / 16;          // MFMA k-steps per k-tile
+    static constexpr int BVX = 64 * NB;             // output voxels per workgroup
+    static constexpr int WTILE = kBCh * ROWB;       // bytes of one W tile
+    static constexpr int XTILE = BVX * ROWB;        // bytes of one X tile
+    static constexpr int STAGE = WTILE + XTILE;     // W tile, then X tile
+    static constexpr int WJ = WTILE / 1024 / 4;     // W load blocks per wave per k-tile
+    static constexpr int XJ = XTILE / 1024 / 4;     // X load blocks per wave per k-tile
+    static constexpr int LOADS = WJ + XJ;
+    static constexpr int OCC = 2;                   // workgroups per CU
+    static_assert(KB == 32 || KB == 64, "k-tile");
     static_assert(NST * STAGE * OCC <= 160 * 1024, "LDS");
-    static_assert(NST >= 3 && NST <= 4, "ring depth");
+    static_assert(NST >= 2 && NST <= 4, "ring depth");
+    static_assert((NST - 2) * LOADS < 16, "vmcnt immediate");
 };
 
-// Unit u of LDS row r sits in slot u ^ swz(r). Four 64-byte rows span the 64
-// banks, so 16 consecutive rows read at one unit cover 16 different bank
-// groups: rows r and r+4 differ in swz.
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+// Unit u of LDS row r sits in slot u ^ swz(r). 64-byte rows: four rows span
+// the 64 banks and rows r, r+4 differ in swz; 128-byte rows: two rows span
+// the banks and rows r, r+2, ..., r+14 differ in swz. Either way 16
+// consecutive rows read at one unit cover 16 different bank groups.
+template <int KB>
+__host__ __device__ constexpr int swz(int r) { return KB == 32 ? (r >> 2) & 3 : (r >> 1) & 7; }
 
 #if defined(__HIP_DEVICE_COMPILE__)
 // Workgroup barrier for reusing an LDS stage: this wave's LDS reads are
@@ -109,44 +122,45 @@ __device__ __forceinline__ Voxel voxel(int m, int Z, int P, int Q) {
 #endif
 
 // grid: (ceil(M / (64*NB)), ceil(K / 128)); block: 256 threads. SMALLC:
-// C < 32, so that one k-tile can cross several taps.
-template <int NB, int NST, bool SMALLC>
+// C < KB, so that one k-tile can cross several taps.
+template <int NB, int NST, int KB, bool SMALLC>
 __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    using Cf = ConvCfg<NB, NST>;
-    constexpr int STAGE = Cf::STAGE, LOADS = Cf::LOADS;
+    using Cf = ConvCfg<NB, NST, KB>;
+    constexpr int STAGE = Cf::STAGE, LOADS = Cf::LOADS, ROWB = Cf::ROWB, UNITS = Cf::UNITS;
+    constexpr int RPB = Cf::RPB, KSTEPS = Cf::KSTEPS, WJ = Cf::WJ, XJ = Cf::XJ;
     // The ring's stages are separate arrays, so that the compiler can tell
     // their accesses apart: a read of one stage never waits for the loads
     // into another.
     __shared__ __attribute__((aligned(1024))) char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) char st1[STAGE];
-    __shared__ __attribute__((aligned(1024))) char st2[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[NST > 2 ? STAGE : 16];
     __shared__ __attribute__((aligned(1024))) char st3[NST > 3 ? STAGE : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m0 = blockIdx.x * Cf::BVX, k0 = blockIdx.y * kBCh;
 
-    // Load roles. LDS block b (1 KB) holds rows 16b..16b+15 of a tile; lane l
-    // writes row 16b + l/4, slot l%4, so it fetches unit
-    // u = (l%4) ^ swz(row) = (l%4) ^ ((l/16) & 3): the same in all of the
-    // lane's blocks (W blocks wave + 4j, j < 2; X blocks wave + 4j, j < NB),
-    // and so is the tap of its reduction group.
-    const int rsub = lane >> 2;
-    const int u = (lane & 3) ^ ((lane >> 4) & 3);
-    unsigned wo[2];  // bytes into w (unused, and possibly wrapped, for rows past K)
-    bool wv[2];
+    // Load roles. LDS block b (1 KB) holds rows RPB*b..RPB*b+RPB-1 of a tile;
+    // lane l writes row RPB*b + l/UNITS, slot l%UNITS, so it fetches unit
+    // u = (l%UNITS) ^ swz(row). For the lane's blocks (W blocks wave + 4j,
+    // j < WJ; X blocks wave + 4j, j < XJ) swz(row) does not depend on j, so u
+    // and the tap of the lane's reduction group are the same in all of them.
+    const int rsub = lane / UNITS;
+    const int u = (lane % UNITS) ^ swz<KB>(RPB * wave + rsub);
+    unsigned wo[WJ];  // bytes into w (unused, and possibly wrapped, for rows past K)
+    bool wv[WJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int k = k0 + 16 * (wave + 4 * j) + rsub;
+    for (int j = 0; j < WJ; ++j) {
+        const int k = k0 + RPB * (wave + 4 * j) + rsub;
         wv[j] = k < a.K;
         wo[j] = ((unsigned)k * (unsigned)a.KG + 8u * (unsigned)u) * 2u;
     }
-    int xo[NB];
-    bool xv[NB];
+    int xo[XJ];
+    bool xv[XJ];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int m = m0 + 16 * (wave + 4 * j) + rsub;
+    for (int j = 0; j < XJ; ++j) {
+        const int m = m0 + RPB * (wave + 4 * j) + rsub;
         xv[j] = m < a.M;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         xo[j] = (int)(v.n * a.xsn + (long long)v.z * a.sd * a.xsd +
@@ -171,10 +185,10 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
         const int tt = tp / (a.S * a.R);
         toff = (int)(tt * a.xsd + tr * a.xsh + ts * a.xsw);
     }
-    // Per k-tile the group moves kBR = tstep*C + cstep elements on: whole taps
-    // (C < 32 only), then cstep channels with at most one more tap.
-    const int tstep = SMALLC ? kBR / a.C : 0;
-    const int cstep = kBR - tstep * a.C;
+    // Per k-tile the group moves KB = tstep*C + cstep elements on: whole taps
+    // (C < KB only), then cstep channels with at most one more tap.
+    const int tstep = SMALLC ? KB / a.C : 0;
+    const int cstep = KB - tstep * a.C;
     const int dr = (int)(a.xsh - a.S * a.xsw), dt = (int)(a.xsd - a.R * a.xsh);
     // Next tap where `go` holds: s, then r, then t.
     auto next_tap = [&](bool go) __attribute__((always_inline)) {
@@ -189,28 +203,28 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
         toff += wr ? dt : 0;
     };
 
-    // Loads of the next k-tile (reduction indices i0 .. i0+31) into an LDS
-    // stage, then the lane's group moves on by kBR.
+    // Loads of the next k-tile (reduction indices i0 .. i0+KB-1) into an LDS
+    // stage, then the lane's group moves on by KB.
     int i0 = 0;
     auto issue = [&](char* dst) __attribute__((always_inline)) {
         const bool kin = gi < a.KG;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < WJ; ++j) {
             const unsigned ow = (wv[j] && kin) ? wo[j] + 2u * (unsigned)i0 : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rw, (LDS_AS void*)(dst + (wave + 4 * j) * 1024), 16, (int)ow, 0, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
+        for (int j = 0; j < XJ; ++j) {
             const unsigned ox = (xv[j] && kin) ? (unsigned)(2 * (xo[j] + toff + cc)) : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rx, (LDS_AS void*)(dst + kWTile + (wave + 4 * j) * 1024), 16, (int)ox, 0, 0, 0);
+                rx, (LDS_AS void*)(dst + Cf::WTILE + (wave + 4 * j) * 1024), 16, (int)ox, 0, 0, 0);
         }
-        i0 += kBR;
-        gi += kBR;
-        if (SMALLC) {  // tstep <= 4 for C >= 8
+        i0 += KB;
+        gi += KB;
+        if (SMALLC) {  // tstep <= KB / 8 for C >= 8
 #pragma unroll
-            for (int i = 0; i < 4; ++i) next_tap(i < tstep);
+            for (int i = 0; i < KB / 8; ++i) next_tap(i < tstep);
         }
         cc += cstep;
         const bool wrap = cc >= a.C;
@@ -222,18 +236,18 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
     // unit 2*ks + l/32 (16 reduction elements per k-step).
     const int g = lane >> 5, r32 = lane & 31;
     const int wch = wave & 1, wvx = wave >> 1;  // channel half, voxel half
-    int aaddr[2][2], baddr[NB][2];
+    int aaddr[2][KSTEPS], baddr[NB][KSTEPS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
         for (int bl = 0; bl < 2; ++bl) {
             const int ra = wch * 64 + bl * 32 + r32;
-            aaddr[bl][ks] = ra * kRowB + (((2 * ks + g) ^ swz(ra)) * 16);
+            aaddr[bl][ks] = ra * ROWB + (((2 * ks + g) ^ swz<KB>(ra)) * 16);
         }
 #pragma unroll
         for (int bl = 0; bl < NB; ++bl) {
             const int rb = wvx * 32 * NB + bl * 32 + r32;
-            baddr[bl][ks] = kWTile + rb * kRowB + (((2 * ks + g) ^ swz(rb)) * 16);
+            baddr[bl][ks] = Cf::WTILE + rb * ROWB + (((2 * ks + g) ^ swz<KB>(rb)) * 16);
         }
     }
 
@@ -252,16 +266,16 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | ((NST - 2) * LOADS));
         lds_barrier();    // every wave's; the k-tile in fill was consumed
         issue(fill);
-        f16x8 af[2][2], bf[2][NB];
+        f16x8 af[KSTEPS][2], bf[KSTEPS][NB];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
             for (int bl = 0; bl < 2; ++bl) af[ks][bl] = lds_read16(cur, aaddr[bl][ks]);
 #pragma unroll
             for (int bl = 0; bl < NB; ++bl) bf[ks][bl] = lds_read16(cur, baddr[bl][ks]);
         }
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -271,10 +285,15 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
     };
     // k-tile t sits in stage t % NST. The loop runs whole groups of NST
     // k-tiles: k-tiles past the end load zeros and add nothing.
-    const int nkt = (a.KG + kBR - 1) / kBR;
+    const int nkt = (a.KG + KB - 1) / KB;
     issue(st0);
-    issue(st1);
-    if constexpr (NST == 4) {
+    if constexpr (NST == 2) {
+        for (int kt = 0; kt < nkt; kt += 2) {
+            step(st1, st0);
+            step(st0, st1);
+        }
+    } else if constexpr (NST == 4) {
+        issue(st1);
         issue(st2);
         for (int kt = 0; kt < nkt; kt += 4) {
             step(st3, st0);
@@ -283,6 +302,7 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
             step(st2, st3);
         }
     } else {
+        issue(st1);
         for (int kt = 0; kt < nkt; kt += 3) {
             step(st2, st0);
             step(st0, st1);
@@ -318,15 +338,15 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 #endif
 }
 
-// Launches configuration (NB, NST) over the whole problem.
-template <int NB, int NST>
+// Launches configuration (NB, NST, KB) over the whole problem.
+template <int NB, int NST, int KB>
 void launch_cfg(const ConvArgs& a, hipStream_t stream) {
-    dim3 grid((unsigned)((a.M + ConvCfg<NB, NST>::BVX - 1) / ConvCfg<NB, NST>::BVX),
-              (unsigned)((a.K + kBCh - 1) / kBCh));
-    if (a.C < kBR)
-        hipLaunchKernelGGL((conv3d_mfma<NB, NST, true>), grid, dim3(kNT), 0, stream, a);
+    using Cf = ConvCfg<NB, NST, KB>;
+    dim3 grid((unsigned)((a.M + Cf::BVX - 1) / Cf::BVX), (unsigned)((a.K + kBCh - 1) / kBCh));
+    if (a.C < KB)
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, true>), grid, dim3(kNT), 0, stream, a);
     else
-        hipLaunchKernelGGL((conv3d_mfma<NB, NST, false>), grid, dim3(kNT), 0, stream, a);
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, false>), grid, dim3(kNT), 0, stream, a);
 }
 
 thread_local char g_err[256];
@@ -344,18 +364,35 @@ int fail(const char* msg) {
 
 bool mult8(long v) { return v >= 0 && v % 8 == 0; }
 
-// Voxel-tile width (NB 32-voxel blocks per wave, 64*NB voxels per workgroup)
-// for an M x K problem. Wider tiles read fewer LDS bytes and pass fewer
-// barriers per MFMA; narrower ones fill the CUs better when the tile count is
-// small or just past a multiple of the workgroup slots (2 per CU). Estimated
-// time: workgroup rounds at half-round granularity (a CU running a single
-// workgroup finishes it sooner) x tile width x relative cost per voxel,
-// measured on MI355X as 1.19 / 1.05 / 1.0 for NB = 2 / 3 / 4.
-// GFX906_AMD_CONV_NB = 2, 3 or 4 overrides the choice (testing).
-int pick_nb(long M, int K) {
-    const char* e = getenv("GFX906_AMD_CONV_NB");
-    const int forced = e ? atoi(e) : 0;
-    if (forced >= 2 && forced <= 4) return forced;
+// Kernel configuration for an M x K problem with reduction length KG: NB
+// (32-voxel blocks per wave, 64*NB voxels per workgroup) and KB (k-tile
+// width). Wider voxel tiles read fewer LDS bytes and pass fewer barriers per
+// MFMA; narrower ones fill the CUs better when the tile count is small or
+// just past a multiple of the workgroup slots (2 per CU). 64-wide k-tiles
+// fetch whole 128-byte lines (32-wide ones half lines) but leave room for
+// only two LDS stages, whose start-up shows on short reductions.
+// Estimated time: the workgroups on the busiest CU, in half rounds (two run
+// at a time; one on its own finishes sooner) x tile width x relative cost per
+// voxel, measured on MI355X:
+//  - KG < 2048: KB = 32 with costs 1.19 / 1.05 / 1.0 for NB = 2 / 3 / 4;
+//  - KG >= 2048: NB = 2 or 3 with KB = 64 (cost 1.0), or NB = 4 with KB = 32
+//    (1.04); a workgroup that runs alone on its CU at the end counts 1.3
+//    halves, as a two-stage ring on its own hides less of its load latency.
+// GFX906_AMD_CONV_CFG = "<NB>x<KB>" (2x32, 3x32, 4x32, 2x64 or 3x64)
+// overrides the choice (testing); it is read on every call.
+struct ConvPick {
+    int nb, kb;
+};
+
+bool valid_cfg(int nb, int kb) {
+    return (kb == 32 && nb >= 2 && nb <= 4) || (kb == 64 && nb >= 2 && nb <= 3);
+}
+
+ConvPick pick_cfg(long M, int K, long KG) {
+    if (const char* e = getenv("GFX906_AMD_CONV_CFG")) {
+        int nb = 0, kb = 0;
+        if (sscanf(e, "%dx%d", &nb, &kb) == 2 && valid_cfg(nb, kb)) return {nb, kb};
+    }
     static const int slots = [] {
         int dev = 0, ncu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -364,17 +401,22 @@ int pick_nb(long M, int K) {
             ncu = 256;
         return 2 * ncu;
     }();
-    const double rel[5] = {0, 0, 1.19, 1.05, 1.0};
     const long kt = (K + kBCh - 1) / kBCh;
-    int best = 4;
+    const bool longk = KG >= 2048;
+    const ConvPick cand[3] = {{4, 32}, {3, longk ? 64 : 32}, {2, longk ? 64 : 32}};
+    const double rel_short[3] = {1.0, 1.05, 1.19}, rel_long[3] = {1.04, 1.0, 1.0};
+    ConvPick best = cand[0];
     double best_cost = 1e300;
-    for (int nb = 4; nb >= 2; --nb) {
+    for (int i = 0; i < 3; ++i) {
+        const int nb = cand[i].nb;
         const long tiles = (M + 64 * nb - 1) / (64 * nb) * kt;
-        const double halves = (double)((2 * tiles + slots - 1) / slots);
-        const double cost = halves * nb * rel[nb];
+        // The busiest CU runs n workgroups, two at a time.
+        const long n = (2 * tiles + slots - 1) / slots;
+        const double halves = (double)n + (longk && (n & 1) ? 0.3 : 0.0);
+        const double cost = halves * nb * (longk ? rel_long[i] : rel_short[i]);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
-            best = nb;
+            best = cand[i];
         }
     }
     return best;
@@ -445,13 +487,15 @@ extern "C" int conv3d_fwd(const void* x, const void* w, const void* bias, const 
     a.rsq = rsq;
     a.x_bytes = (unsigned)x_span;
     a.w_bytes = (unsigned)w_span;
-    const int nb = pick_nb(M, K);
-    if (nb == 2)
-        launch_cfg<2, 4>(a, stream);
-    else if (nb == 3)
-        launch_cfg<3, 4>(a, stream);
+    const ConvPick c = pick_cfg(M, K, KG);
+    if (c.kb == 64)
+        c.nb == 2 ? launch_cfg<2, 2, 64>(a, stream) : launch_cfg<3, 2, 64>(a, stream);
+    else if (c.nb == 2)
+        launch_cfg<2, 4, 32>(a, stream);
+    else if (c.nb == 3)
+        launch_cfg<3, 4, 32>(a, stream);
     else
-        launch_cfg<4, 3>(a, stream);
+        launch_cfg<4, 3, 32>(a, stream);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));

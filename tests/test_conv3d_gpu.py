@@ -60,36 +60,46 @@ def test_reference_cases(i):
     assert got.is_contiguous(memory_format=CL)
 
 
-@pytest.mark.parametrize("nb", [2, 3, 4])
-@pytest.mark.parametrize("i", [0, 3, 5, 6, 7, 9])
-def test_every_tile_width(monkeypatch, nb, i):
-    """Each voxel-tile width the launcher can pick (GFX906_AMD_CONV_NB forces
-    it), on cases with partial voxel and channel tiles, strides, C = 8
-    (several taps per k-tile) and a 1x3x3 window."""
-    monkeypatch.setenv("GFX906_AMD_CONV_NB", str(nb))
-    xs, ws, stride, has_b, has_r = oc.REF_CASES[i]
-    x, w, b, res = oc.make_case(xs, ws, stride, has_b, has_r, seed=200 + i)
+CFGS = ["2x32", "3x32", "4x32", "2x64", "3x64"]  # <NB>x<KB> the launcher can pick
+# C = 24 and 40: several taps per 64-wide k-tile, not a divisor of it
+EXTRA_CASES = [((1, 24, 3, 12, 12), (32, 3, 3, 3), (1, 1, 1), True, False),
+               ((1, 40, 4, 10, 14), (48, 3, 3, 3), (1, 1, 1), False, True)]
+
+
+@pytest.mark.parametrize("cfg", CFGS)
+@pytest.mark.parametrize("i", [0, 3, 5, 6, 7, 9, "x0", "x1"])
+def test_every_kernel_config(monkeypatch, cfg, i):
+    """Each kernel configuration the launcher can pick (GFX906_AMD_CONV_CFG
+    forces it), on cases with partial voxel and channel tiles, strides,
+    C = 8 (several taps per k-tile), C = 24 / 40 / 96 (taps that start
+    inside a k-tile) and a 1x3x3 window."""
+    monkeypatch.setenv("GFX906_AMD_CONV_CFG", cfg)
+    case = EXTRA_CASES[int(i[1:])] if isinstance(i, str) else oc.REF_CASES[i]
+    xs, ws, stride, has_b, has_r = case
+    seed = 300 + int(i[1:]) if isinstance(i, str) else 200 + i
+    x, w, b, res = oc.make_case(xs, ws, stride, has_b, has_r, seed=seed)
     xd = to_dev(x).contiguous(memory_format=CL)
     wd = to_dev(w).contiguous(memory_format=CL)
     rd = None if res is None else to_dev(res).contiguous(memory_format=CL)
     got = direct(xd, wd, to_dev(b), rd, stride)
     torch.cuda.synchronize()
-    check(got, oc.conv3d_gemm(x, w, b, res, stride), f"nb{nb} case{i} {xs}->{ws} st{stride}")
+    check(got, oc.conv3d_gemm(x, w, b, res, stride), f"{cfg} case{i} {xs}->{ws} st{stride}")
 
 
-@pytest.mark.parametrize("nb", [2, 3, 4])
-def test_tile_widths_agree_bitwise_on_vae_shape(monkeypatch, nb):
-    """The reduction order does not depend on the tile width: every width
-    gives the same bits on a VAE-sized layer (checked against NB = 4)."""
+@pytest.mark.parametrize("cfg", CFGS)
+def test_kernel_configs_agree_bitwise_on_vae_shape(monkeypatch, cfg):
+    """The reduction order depends on neither the tile width nor the k-tile
+    width: every configuration gives the same bits on a VAE-sized layer
+    (checked against 4x32)."""
     g = torch.Generator().manual_seed(5)
     x = (torch.randn(1, 256, 5, 40, 40, generator=g) * 0.25).half().to(DEV).contiguous(
         memory_format=CL)
     w = (torch.randn(256, 256, 3, 3, 3, generator=g) * 0.25).half().to(DEV).contiguous(
         memory_format=CL)
     b = torch.randn(256, generator=g).half().to(DEV)
-    monkeypatch.setenv("GFX906_AMD_CONV_NB", "4")
+    monkeypatch.setenv("GFX906_AMD_CONV_CFG", "4x32")
     ref = direct(x, w, b, None, (1, 1, 1))
-    monkeypatch.setenv("GFX906_AMD_CONV_NB", str(nb))
+    monkeypatch.setenv("GFX906_AMD_CONV_CFG", cfg)
     got = direct(x, w, b, None, (1, 1, 1))
     torch.cuda.synchronize()
     assert torch.equal(got, ref)

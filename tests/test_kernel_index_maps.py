@@ -7,7 +7,10 @@ kernel source (the GPU parity tests check the kernels themselves):
   4e + i/4, e = 0..3) and the V^T reads deliver exactly the MFMA operands, P's
   key order matches V^T's, and no read pattern has LDS bank conflicts;
 * conv3d's incremental tap tracking (conv3d_mfma) agrees with the direct
-  division-based index for every k-tile and lane group.
+  division-based index for every k-tile and lane group, and its load roles
+  for both k-tile widths (32 and 64 reduction elements) fill every LDS slot
+  once, with whole rows fetched by neighbouring lanes and conflict-free
+  operand reads.
 """
 
 import numpy as np
@@ -122,7 +125,7 @@ def tap_walk(C, T, R, S, xsd, xsh, xsw, kbr=32):
     KG = C * T * R * S
     nkt = -(-KG // kbr)
     small = C < kbr
-    for u in range(4):
+    for u in range(kbr // 8):
         gi = 8 * u
         tp = gi // C
         cc, ts, tr = gi - tp * C, tp % S, (tp // S) % R
@@ -147,7 +150,7 @@ def tap_walk(C, T, R, S, xsd, xsh, xsw, kbr=32):
             yield gi, cc, toff, KG
             gi += kbr
             if small:
-                for i in range(4):
+                for i in range(kbr // 8):
                     next_tap(i < tstep)
             cc += cstep
             wrap = cc >= C
@@ -155,14 +158,55 @@ def tap_walk(C, T, R, S, xsd, xsh, xsw, kbr=32):
             next_tap(wrap)
 
 
-@pytest.mark.parametrize("C", [8, 16, 24, 32, 40, 64, 96, 512])
+@pytest.mark.parametrize("kbr", [32, 64])
+@pytest.mark.parametrize("C", [8, 16, 24, 32, 40, 56, 64, 96, 512])
 @pytest.mark.parametrize("trs", [(1, 1, 1), (3, 3, 3), (1, 3, 3), (2, 3, 2), (5, 2, 3)])
-def test_conv3d_tap_tracking_matches_division(C, trs):
+def test_conv3d_tap_tracking_matches_division(C, trs, kbr):
     T, R, S = trs
     xsd, xsh, xsw = 7919 * C, 131 * C, C
-    for gi, cc, toff, KG in tap_walk(C, T, R, S, xsd, xsh, xsw):
+    for gi, cc, toff, KG in tap_walk(C, T, R, S, xsd, xsh, xsw, kbr):
         if gi >= KG:
             continue
         tp = gi // C
         t, r, s = tp // (R * S), (tp // S) % R, tp % S
         assert (cc, toff) == (gi % C, t * xsd + r * xsh + s * xsw)
+
+
+def conv_swz(kb, r):
+    return (r >> 2) & 3 if kb == 32 else (r >> 1) & 7
+
+
+@pytest.mark.parametrize("kb", [32, 64])
+@pytest.mark.parametrize("nb", [2, 3, 4])
+def test_conv3d_load_roles_and_operand_reads(kb, nb):
+    rowb, units = 2 * kb, kb // 8
+    rpb = 1024 // rowb
+    wtile, xtile = 128 * rowb, 64 * nb * rowb
+    for tile_bytes, nblk in ((wtile, wtile // 4096), (xtile, xtile // 4096)):
+        seen = {}
+        for wave in range(4):
+            for lane in range(64):
+                rsub = lane // units
+                u = (lane % units) ^ conv_swz(kb, rpb * wave + rsub)
+                for j in range(nblk):
+                    blk = wave + 4 * j
+                    row, slot = rpb * blk + rsub, lane % units
+                    assert blk * 1024 + 16 * lane == row * rowb + 16 * slot
+                    assert u == slot ^ conv_swz(kb, row)  # same unit in every block j
+                    seen[(row, slot)] = u
+        rows = tile_bytes // rowb
+        assert len(seen) == rows * units  # every slot written once
+        # neighbouring lanes fetch whole rows: all units of a row, each once
+        for row in range(rows):
+            assert sorted(seen[(row, sl)] for sl in range(units)) == list(range(units))
+        # operand reads: row base + l%32, unit 2ks + l/32, 16 lanes served together
+        for base in range(0, rows, 32):
+            for ks in range(kb // 16):
+                for q in range(4):
+                    addrs = []
+                    for lane in range(16 * q, 16 * q + 16):
+                        r, unit = base + lane % 32, 2 * ks + lane // 32
+                        slot = unit ^ conv_swz(kb, r)
+                        assert seen[(r, slot)] == unit  # the read finds its unit
+                        addrs.append(r * rowb + 16 * slot)
+                    assert conflict_free(addrs, 16)
