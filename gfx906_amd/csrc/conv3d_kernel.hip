@@ -12,10 +12,12 @@
 //    the A operand of v_mfma_f32_32x32x16_f16, a lane's accumulator holds
 //    four runs of four consecutive output channels of one voxel: the
 //    channels-innermost output, bias and residual move as 8-byte vectors.
-//  * Tiles of 128 channels x 64*NB voxels x KB reduction elements (NB = 2, 3
-//    or 4 and KB = 32 or 64, chosen per problem for how the tile count fills
-//    the CUs and how long the reduction is), 4 waves of 64 x 32*NB (2 x NB
-//    MFMA blocks), two workgroups per CU whose barriers are independent.
+//  * Tiles of 64*CW channels x 64*NB voxels x KB reduction elements (CW = 2
+//    or 4, NB = 2, 3 or 4, KB = 32 or 64; six configurations, chosen per
+//    problem for how the tile count fills the CUs and how long the
+//    reduction is), 2*CW waves of 64 x 32*NB (2 x NB MFMA blocks): with
+//    CW = 2 two workgroups per CU whose barriers are independent, with
+//    CW = 4 one workgroup of 8 waves that loads fewer bytes per MFMA.
 //    Both operand tiles go from HBM into LDS with buffer loads to LDS (no
 //    VGPR staging); the input gather uses a per-lane offset (voxel base +
 //    the offset of the lane's tap, advanced incrementally from k-tile to
@@ -54,30 +56,34 @@ struct ConvArgs {
     unsigned x_bytes, w_bytes;
 };
 
-constexpr int kBCh = 128;              // output channels per workgroup (GEMM rows)
-constexpr int kNT = 256;               // 4 waves: 2 along channels x 2 along voxels
 constexpr int kMaxTaps = 1024;
 constexpr unsigned kOOB = 0xFFFFFFF0u;  // buffer offset past any range: loads zeros
 
-// Per-configuration sizes: NB 32-voxel MFMA blocks per wave (64*NB voxels per
+// Per-configuration sizes: NB 32-voxel MFMA blocks per wave, CW waves along
+// output channels x 2 along voxels (64*CW channels x 64*NB voxels per
 // workgroup), NST stages in the LDS ring, KB reduction elements per k-tile
 // (LDS rows of 2*KB bytes: 32 -> 64-byte rows, 64 -> 128-byte rows, so that
 // each row of a tile is one whole 128-byte line of the weights or of a voxel).
-template <int NB, int NST, int KB>
+template <int NB, int NST, int KB, int CW>
 struct ConvCfg {
+    static constexpr int NW = 2 * CW;               // waves
+    static constexpr int NT = 64 * NW;              // threads
+    static constexpr int BCH = 64 * CW;             // output channels per workgroup
     static constexpr int ROWB = 2 * KB;             // bytes per LDS row
     static constexpr int UNITS = ROWB / 16;         // 16-byte units per row
     static constexpr int RPB = 1024 / ROWB;         // rows per 1 KB load block
     static constexpr int KSTEPS = KB / 16;          // MFMA k-steps per k-tile
     static constexpr int BVX = 64 * NB;             // output voxels per workgroup
-    static constexpr int WTILE = kBCh * ROWB;       // bytes of one W tile
+    static constexpr int WTILE = BCH * ROWB;        // bytes of one W tile
     static constexpr int XTILE = BVX * ROWB;        // bytes of one X tile
     static constexpr int STAGE = WTILE + XTILE;     // W tile, then X tile
-    static constexpr int WJ = WTILE / 1024 / 4;     // W load blocks per wave per k-tile
-    static constexpr int XJ = XTILE / 1024 / 4;     // X load blocks per wave per k-tile
+    static constexpr int WJ = WTILE / 1024 / NW;    // W load blocks per wave per k-tile
+    static constexpr int XJ = XTILE / 1024 / NW;    // X load blocks per wave per k-tile
     static constexpr int LOADS = WJ + XJ;
-    static constexpr int OCC = 2;                   // workgroups per CU
+    static constexpr int OCC = CW == 2 ? 2 : 1;     // workgroups per CU
     static_assert(KB == 32 || KB == 64, "k-tile");
+    static_assert(CW == 2 || CW == 4, "channel waves");
+    static_assert(WJ * NW * 1024 == WTILE && XJ * NW * 1024 == XTILE, "whole load blocks");
     static_assert(NST * STAGE * OCC <= 160 * 1024, "LDS");
     static_assert(NST >= 2 && NST <= 4, "ring depth");
     static_assert((NST - 2) * LOADS < 16, "vmcnt immediate");
@@ -121,14 +127,26 @@ __device__ __forceinline__ Voxel voxel(int m, int Z, int P, int Q) {
 }
 #endif
 
-// grid: (ceil(M / (64*NB)), ceil(K / 128)); block: 256 threads. SMALLC:
-// C < KB, so that one k-tile can cross several taps.
-template <int NB, int NST, int KB, bool SMALLC>
-__global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
+// Tile (voxel tile * channel tiles + channel tile) of workgroup L of n.
+// Workgroups go to the 8 XCDs round robin (L % 8), each XCD with its own L2;
+// this map gives XCD x the x-th contiguous eighth of the tiles, in order, so
+// that the channel tiles of one voxel tile, and neighbouring voxel tiles
+// (whose input windows overlap), share one L2.
+__device__ __forceinline__ int tile_of(int L, int n) {
+    const int xcd = L & 7, pos = L >> 3, base = n >> 3, extra = n & 7;
+    return (xcd < extra ? xcd * (base + 1) : extra * (base + 1) + (xcd - extra) * base) + pos;
+}
+
+// grid: ceil(M / (64*NB)) * ceil(K / (64*CW)) workgroups (1-D, see tile_of);
+// block: 128*CW threads. SMALLC: C < KB, so that one k-tile can cross
+// several taps.
+template <int NB, int NST, int KB, int CW, bool SMALLC>
+__global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT), (ConvCfg<NB, NST, KB, CW>::OCC))
+    conv3d_mfma(const ConvArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    using Cf = ConvCfg<NB, NST, KB>;
+    using Cf = ConvCfg<NB, NST, KB, CW>;
     constexpr int STAGE = Cf::STAGE, LOADS = Cf::LOADS, ROWB = Cf::ROWB, UNITS = Cf::UNITS;
-    constexpr int RPB = Cf::RPB, KSTEPS = Cf::KSTEPS, WJ = Cf::WJ, XJ = Cf::XJ;
+    constexpr int RPB = Cf::RPB, KSTEPS = Cf::KSTEPS, WJ = Cf::WJ, XJ = Cf::XJ, NW = Cf::NW;
     // The ring's stages are separate arrays, so that the compiler can tell
     // their accesses apart: a read of one stage never waits for the loads
     // into another.
@@ -139,20 +157,26 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m0 = blockIdx.x * Cf::BVX, k0 = blockIdx.y * kBCh;
+    int m0, k0;
+    {
+        const int nct = (a.K + Cf::BCH - 1) / Cf::BCH;
+        const int t = tile_of(blockIdx.x, gridDim.x), vt = t / nct;
+        m0 = vt * Cf::BVX;
+        k0 = (t - vt * nct) * Cf::BCH;
+    }
 
     // Load roles. LDS block b (1 KB) holds rows RPB*b..RPB*b+RPB-1 of a tile;
     // lane l writes row RPB*b + l/UNITS, slot l%UNITS, so it fetches unit
-    // u = (l%UNITS) ^ swz(row). For the lane's blocks (W blocks wave + 4j,
-    // j < WJ; X blocks wave + 4j, j < XJ) swz(row) does not depend on j, so u
-    // and the tap of the lane's reduction group are the same in all of them.
+    // u = (l%UNITS) ^ swz(row). For the lane's blocks (W blocks wave + NW*j,
+    // j < WJ; X blocks wave + NW*j, j < XJ) swz(row) does not depend on j, so
+    // u and the tap of the lane's reduction group are the same in all of them.
     const int rsub = lane / UNITS;
     const int u = (lane % UNITS) ^ swz<KB>(RPB * wave + rsub);
     unsigned wo[WJ];  // bytes into w (unused, and possibly wrapped, for rows past K)
     bool wv[WJ];
 #pragma unroll
     for (int j = 0; j < WJ; ++j) {
-        const int k = k0 + RPB * (wave + 4 * j) + rsub;
+        const int k = k0 + RPB * (wave + NW * j) + rsub;
         wv[j] = k < a.K;
         wo[j] = ((unsigned)k * (unsigned)a.KG + 8u * (unsigned)u) * 2u;
     }
@@ -160,7 +184,7 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
     bool xv[XJ];
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
-        const int m = m0 + RPB * (wave + 4 * j) + rsub;
+        const int m = m0 + RPB * (wave + NW * j) + rsub;
         xv[j] = m < a.M;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         xo[j] = (int)(v.n * a.xsn + (long long)v.z * a.sd * a.xsd +
@@ -212,13 +236,13 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
         for (int j = 0; j < WJ; ++j) {
             const unsigned ow = (wv[j] && kin) ? wo[j] + 2u * (unsigned)i0 : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (LDS_AS void*)(dst + (wave + 4 * j) * 1024), 16, (int)ow, 0, 0, 0);
+                rw, (LDS_AS void*)(dst + (wave + NW * j) * 1024), 16, (int)ow, 0, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < XJ; ++j) {
             const unsigned ox = (xv[j] && kin) ? (unsigned)(2 * (xo[j] + toff + cc)) : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rx, (LDS_AS void*)(dst + Cf::WTILE + (wave + 4 * j) * 1024), 16, (int)ox, 0, 0, 0);
+                rx, (LDS_AS void*)(dst + Cf::WTILE + (wave + NW * j) * 1024), 16, (int)ox, 0, 0, 0);
         }
         i0 += KB;
         gi += KB;
@@ -235,7 +259,7 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
     // MFMA operand addresses: lane l reads row (32-row block base + l%32),
     // unit 2*ks + l/32 (16 reduction elements per k-step).
     const int g = lane >> 5, r32 = lane & 31;
-    const int wch = wave & 1, wvx = wave >> 1;  // channel half, voxel half
+    const int wch = wave % CW, wvx = wave / CW;  // channel quarter/half, voxel half
     int aaddr[2][KSTEPS], baddr[NB][KSTEPS];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -338,15 +362,18 @@ __global__ void __launch_bounds__(kNT, 2) conv3d_mfma(const ConvArgs a) {
 #endif
 }
 
-// Launches configuration (NB, NST, KB) over the whole problem.
-template <int NB, int NST, int KB>
+// Launches configuration (NB, NST, KB, CW) over the whole problem.
+template <int NB, int NST, int KB, int CW>
 void launch_cfg(const ConvArgs& a, hipStream_t stream) {
-    using Cf = ConvCfg<NB, NST, KB>;
-    dim3 grid((unsigned)((a.M + Cf::BVX - 1) / Cf::BVX), (unsigned)((a.K + kBCh - 1) / kBCh));
+    using Cf = ConvCfg<NB, NST, KB, CW>;
+    const unsigned tiles = (unsigned)((a.M + Cf::BVX - 1) / Cf::BVX) *
+                           (unsigned)((a.K + Cf::BCH - 1) / Cf::BCH);
     if (a.C < KB)
-        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, true>), grid, dim3(kNT), 0, stream, a);
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, CW, true>), dim3(tiles), dim3(Cf::NT), 0,
+                           stream, a);
     else
-        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, false>), grid, dim3(kNT), 0, stream, a);
+        hipLaunchKernelGGL((conv3d_mfma<NB, NST, KB, CW, false>), dim3(tiles), dim3(Cf::NT), 0,
+                           stream, a);
 }
 
 thread_local char g_err[256];
@@ -364,59 +391,73 @@ int fail(const char* msg) {
 
 bool mult8(long v) { return v >= 0 && v % 8 == 0; }
 
-// Kernel configuration for an M x K problem with reduction length KG: NB
-// (32-voxel blocks per wave, 64*NB voxels per workgroup) and KB (k-tile
-// width). Wider voxel tiles read fewer LDS bytes and pass fewer barriers per
-// MFMA; narrower ones fill the CUs better when the tile count is small or
-// just past a multiple of the workgroup slots (2 per CU). 64-wide k-tiles
-// fetch whole 128-byte lines (32-wide ones half lines) but leave room for
-// only two LDS stages, whose start-up shows on short reductions.
-// Estimated time: the workgroups on the busiest CU, in half rounds (two run
-// at a time; one on its own finishes sooner) x tile width x relative cost per
-// voxel, measured on MI355X:
-//  - KG < 2048: KB = 32 with costs 1.19 / 1.05 / 1.0 for NB = 2 / 3 / 4;
-//  - KG >= 2048: NB = 2 or 3 with KB = 64 (cost 1.0), or NB = 4 with KB = 32
-//    (1.04); a workgroup that runs alone on its CU at the end counts 1.3
-//    halves, as a two-stage ring on its own hides less of its load latency.
-// GFX906_AMD_CONV_CFG = "<NB>x<KB>" (2x32, 3x32, 4x32, 2x64 or 3x64)
-// overrides the choice (testing); it is read on every call.
-struct ConvPick {
-    int nb, kb;
+// The kernel configurations: NB, KB, channels per workgroup (64*CW),
+// workgroups per CU, relative cost per output element and reduction element
+// (fitted on MI355X, see pick_kernel), launcher.
+struct ConvKernel {
+    int nb, kb, bch, occ;
+    double rel;
+    void (*launch)(const ConvArgs&, hipStream_t);
 };
+const ConvKernel kKernels[] = {
+    {4, 32, 128, 2, 6.21, launch_cfg<4, 3, 32, 2>}, {3, 64, 128, 2, 6.18, launch_cfg<3, 2, 64, 2>},
+    {2, 64, 128, 2, 6.68, launch_cfg<2, 2, 64, 2>}, {4, 32, 256, 1, 4.78, launch_cfg<4, 4, 32, 4>},
+    {3, 64, 256, 1, 5.91, launch_cfg<3, 2, 64, 4>}, {2, 64, 256, 1, 5.47, launch_cfg<2, 3, 64, 4>},
+};
+constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
-bool valid_cfg(int nb, int kb) {
-    return (kb == 32 && nb >= 2 && nb <= 4) || (kb == 64 && nb >= 2 && nb <= 3);
+int find_kernel(int nb, int kb, int bch) {
+    for (int i = 0; i < kNumKernels; ++i)
+        if (kKernels[i].nb == nb && kKernels[i].kb == kb && kKernels[i].bch == bch) return i;
+    return -1;
 }
 
-ConvPick pick_cfg(long M, int K, long KG) {
+// Kernel configuration for an M x K problem with reduction length KG. Wider
+// tiles load fewer bytes per MFMA (the loads into LDS, not the matrix cores,
+// bound these kernels); narrower ones fill the CUs better when the tile count
+// is small or just past a multiple of the workgroup slots. 64-wide k-tiles
+// fetch whole 128-byte lines, 32-wide ones half lines but leave room for a
+// deeper ring. Estimated time: R x tile size x (rel x KG / 13824 + 0.355),
+// R the workgroups on the busiest CU in units of one workgroup's time (for
+// two per CU: half rounds, a workgroup left alone on its CU at the end
+// counting 1.3 halves), rel and the per-tile term (start-up and epilogue)
+// fitted to six layers on MI355X (VAE decoder 3x3x3 with 128..512 channels,
+// a 1x1x1). GFX906_AMD_CONV_CFG = "<NB>x<KB>" (128 channels) or
+// "<NB>x<KB>x<channels>" (a row of kKernels) overrides the choice (testing);
+// it is read on every call.
+int pick_kernel(long M, int K, long KG) {
     if (const char* e = getenv("GFX906_AMD_CONV_CFG")) {
-        int nb = 0, kb = 0;
-        if (sscanf(e, "%dx%d", &nb, &kb) == 2 && valid_cfg(nb, kb)) return {nb, kb};
+        int nb = 0, kb = 0, bch = 128;
+        if (sscanf(e, "%dx%dx%d", &nb, &kb, &bch) >= 2) {
+            const int i = find_kernel(nb, kb, bch);
+            if (i >= 0) return i;
+        }
     }
-    static const int slots = [] {
-        int dev = 0, ncu = 0;
+    static const int ncu = [] {
+        int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            ncu <= 0)
-            ncu = 256;
-        return 2 * ncu;
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        return n;
     }();
-    const long kt = (K + kBCh - 1) / kBCh;
-    const bool longk = KG >= 2048;
-    const ConvPick cand[3] = {{4, 32}, {3, longk ? 64 : 32}, {2, longk ? 64 : 32}};
-    const double rel_short[3] = {1.0, 1.05, 1.19}, rel_long[3] = {1.04, 1.0, 1.0};
-    ConvPick best = cand[0];
+    const double kgu = (double)KG / 13824.0;
+    int best = 0;
     double best_cost = 1e300;
-    for (int i = 0; i < 3; ++i) {
-        const int nb = cand[i].nb;
-        const long tiles = (M + 64 * nb - 1) / (64 * nb) * kt;
-        // The busiest CU runs n workgroups, two at a time.
-        const long n = (2 * tiles + slots - 1) / slots;
-        const double halves = (double)n + (longk && (n & 1) ? 0.3 : 0.0);
-        const double cost = halves * nb * (longk ? rel_long[i] : rel_short[i]);
-        if (cost < best_cost * 0.999) {
+    for (int i = 0; i < kNumKernels; ++i) {
+        const ConvKernel& c = kKernels[i];
+        const long tiles = (M + 64 * c.nb - 1) / (64 * c.nb) * ((K + c.bch - 1) / c.bch);
+        double r;
+        if (c.occ == 2) {
+            const long n = (tiles + ncu - 1) / ncu;  // half rounds on the busiest CU
+            r = (double)n + (n & 1 ? 0.3 : 0.0);
+        } else {
+            r = (double)((tiles + ncu - 1) / ncu);
+        }
+        const double cost = r * 64.0 * c.nb * c.bch * (c.rel * kgu + 0.355);
+        if (cost < best_cost) {
             best_cost = cost;
-            best = cand[i];
+            best = i;
         }
     }
     return best;
@@ -487,15 +528,7 @@ extern "C" int conv3d_fwd(const void* x, const void* w, const void* bias, const 
     a.rsq = rsq;
     a.x_bytes = (unsigned)x_span;
     a.w_bytes = (unsigned)w_span;
-    const ConvPick c = pick_cfg(M, K, KG);
-    if (c.kb == 64)
-        c.nb == 2 ? launch_cfg<2, 2, 64>(a, stream) : launch_cfg<3, 2, 64>(a, stream);
-    else if (c.nb == 2)
-        launch_cfg<2, 4, 32>(a, stream);
-    else if (c.nb == 3)
-        launch_cfg<3, 4, 32>(a, stream);
-    else
-        launch_cfg<4, 3, 32>(a, stream);
+    kKernels[pick_kernel(M, K, KG)].launch(a, stream);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));

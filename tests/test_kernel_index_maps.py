@@ -176,20 +176,24 @@ def conv_swz(kb, r):
     return (r >> 2) & 3 if kb == 32 else (r >> 1) & 7
 
 
-@pytest.mark.parametrize("kb", [32, 64])
-@pytest.mark.parametrize("nb", [2, 3, 4])
-def test_conv3d_load_roles_and_operand_reads(kb, nb):
-    rowb, units = 2 * kb, kb // 8
+CONV_KERNELS = [(4, 32, 2), (3, 64, 2), (2, 64, 2), (4, 32, 4), (3, 64, 4), (2, 64, 4)]  # NB, KB, CW
+
+
+@pytest.mark.parametrize("nb,kb,cw", CONV_KERNELS)
+def test_conv3d_load_roles_and_operand_reads(nb, kb, cw):
+    rowb, units, nw = 2 * kb, kb // 8, 2 * cw
     rpb = 1024 // rowb
-    wtile, xtile = 128 * rowb, 64 * nb * rowb
-    for tile_bytes, nblk in ((wtile, wtile // 4096), (xtile, xtile // 4096)):
+    wtile, xtile = 64 * cw * rowb, 64 * nb * rowb
+    for tile_bytes in (wtile, xtile):
+        nblk = tile_bytes // 1024 // nw
+        assert nblk * nw * 1024 == tile_bytes  # whole load blocks per wave
         seen = {}
-        for wave in range(4):
+        for wave in range(nw):
             for lane in range(64):
                 rsub = lane // units
                 u = (lane % units) ^ conv_swz(kb, rpb * wave + rsub)
                 for j in range(nblk):
-                    blk = wave + 4 * j
+                    blk = wave + nw * j
                     row, slot = rpb * blk + rsub, lane % units
                     assert blk * 1024 + 16 * lane == row * rowb + 16 * slot
                     assert u == slot ^ conv_swz(kb, row)  # same unit in every block j
@@ -210,3 +214,17 @@ def test_conv3d_load_roles_and_operand_reads(kb, nb):
                         assert seen[(r, slot)] == unit  # the read finds its unit
                         addrs.append(r * rowb + 16 * slot)
                     assert conflict_free(addrs, 16)
+
+
+def tile_of(L, n):
+    xcd, pos, base, extra = L & 7, L >> 3, n >> 3, n & 7
+    return (xcd * (base + 1) if xcd < extra else extra * (base + 1) + (xcd - extra) * base) + pos
+
+
+@pytest.mark.parametrize("n", [1, 5, 8, 13, 242, 484, 1024, 1490])
+def test_conv3d_xcd_tile_map_is_a_permutation_in_contiguous_eighths(n):
+    tiles = [tile_of(L, n) for L in range(n)]
+    assert sorted(tiles) == list(range(n))
+    for x in range(8):  # XCD x (workgroups L = x mod 8) gets one contiguous run, in order
+        run = tiles[x::8]
+        assert run == list(range(run[0], run[0] + len(run))) if run else True
