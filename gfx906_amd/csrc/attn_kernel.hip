@@ -152,6 +152,17 @@ __device__ __forceinline__ typename Elem<T>::x8 ld_global16(const T* p) {
 
 // Three-way max; with NaN-free arithmetic assumed (-fno-honor-nans) the
 // backend selects v_max3_f32 for it.
+// Workgroup barrier for the LDS ring: this wave's LDS reads and writes are
+// complete (lgkmcnt(0)), then s_barrier. __syncthreads() would add a release
+// fence that also waits for every load to LDS still in flight (vmcnt(0)),
+// which drains the tiles meant to stay in flight across the barrier. Each
+// wave first waits for its own part of the tile it needs (vmcnt(n)); the
+// barrier then orders every wave's part before the reads that follow.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
 __device__ __forceinline__ float max3(float a, float b, float c) {
     return fmaxf(fmaxf(a, b), c);
 }
@@ -341,8 +352,10 @@ __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int 
 // grid: ceil(Sq / BM) * B*H (* nsplit with SPLIT) workgroups, query tiles of
 // one head adjacent (the splits of one query tile adjacent); block: NW*64
 // threads.
+// The second launch bound is HIP's minimum waves per SIMD (amdgpu_waves_per_eu):
+// OCC workgroups of NW waves over the CU's four SIMDs.
 template <class C, bool PAD, class T, bool SPLIT>
-__global__ void __launch_bounds__(C::NT, C::OCC)
+__global__ void __launch_bounds__(C::NT, C::OCC * C::NW / 4)
 attn_fwd_pipe(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
     using E = Elem<T>;
@@ -522,7 +535,7 @@ attn_fwd_pipe(const KArgs a) {
             qk(cur, 1, Sb);    // block 2w+1
             softmax(Sa, Pa);   // block 2w
             __builtin_amdgcn_s_waitcnt(kWaitNext);  // own loads of tile w+1 done
-            __syncthreads();                        // every wave's; tile w-1 consumed
+            lds_barrier();                          // every wave's; tile w-1 consumed
             issue(w + 3, fill);
             mask(Sb, w * C::BN + 32);
             pv(cur, 0, Pa);    // block 2w
@@ -538,7 +551,7 @@ attn_fwd_pipe(const KArgs a) {
         for (int i = tid; i < TILE / 16; i += C::NT)
             *reinterpret_cast<u32x4*>(st3 + TILE + 16 * i) = u32x4{};
         __builtin_amdgcn_s_waitcnt(kWaitNext);
-        __syncthreads();
+        lds_barrier();
         issue(2, st2);
         qk(st0, 0, Sa);
 

@@ -140,8 +140,11 @@ __device__ __forceinline__ int tile_of(int L, int n) {
 // grid: ceil(M / (64*NB)) * ceil(K / (64*CW)) workgroups (1-D, see tile_of);
 // block: 128*CW threads. SMALLC: C < KB, so that one k-tile can cross
 // several taps.
+// The second launch bound is HIP's minimum waves per SIMD (amdgpu_waves_per_eu):
+// OCC workgroups of 2*CW waves over the CU's four SIMDs.
 template <int NB, int NST, int KB, int CW, bool SMALLC>
-__global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT), (ConvCfg<NB, NST, KB, CW>::OCC))
+__global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
+                                  (ConvCfg<NB, NST, KB, CW>::OCC * ConvCfg<NB, NST, KB, CW>::NW / 4))
     conv3d_mfma(const ConvArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
     using Cf = ConvCfg<NB, NST, KB, CW>;
