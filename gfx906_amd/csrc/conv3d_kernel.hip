@@ -13,7 +13,7 @@
 //    four runs of four consecutive output channels of one voxel: the
 //    channels-innermost output, bias and residual move as 8-byte vectors.
 //  * Tiles of 64*CW channels x 64*NB voxels x KB reduction elements (CW = 2
-//    or 4, NB = 2, 3 or 4, KB = 32 or 64; six configurations, chosen per
+//    or 4, NB = 2, 3 or 4, KB = 32 or 64; seven configurations, chosen per
 //    problem for how the tile count fills the CUs and how long the
 //    reduction is), 2*CW waves of 64 x 32*NB (2 x NB MFMA blocks): with
 //    CW = 2 two workgroups per CU whose barriers are independent, with
@@ -76,14 +76,20 @@ struct ConvCfg {
     static constexpr int BVX = 64 * NB;             // output voxels per workgroup
     static constexpr int WTILE = BCH * ROWB;        // bytes of one W tile
     static constexpr int XTILE = BVX * ROWB;        // bytes of one X tile
-    static constexpr int STAGE = WTILE + XTILE;     // W tile, then X tile
     static constexpr int WJ = WTILE / 1024 / NW;    // W load blocks per wave per k-tile
-    static constexpr int XJ = XTILE / 1024 / NW;    // X load blocks per wave per k-tile
+    static constexpr int XBLK = XTILE / 1024;       // X load blocks per k-tile
+    // X load blocks per wave per k-tile. When the waves do not divide the X
+    // blocks, the waves past the last block issue a load of zeros into a
+    // 1 KB pad after the X tile instead, so that every wave issues the same
+    // number of loads and every wait count stays static.
+    static constexpr int XJ = (XBLK + NW - 1) / NW;
+    static constexpr int PAD = XJ * NW > XBLK ? 1024 : 0;
+    static constexpr int STAGE = WTILE + XTILE + PAD;  // W tile, X tile, pad
     static constexpr int LOADS = WJ + XJ;
     static constexpr int OCC = CW == 2 ? 2 : 1;     // workgroups per CU
     static_assert(KB == 32 || KB == 64, "k-tile");
     static_assert(CW == 2 || CW == 4, "channel waves");
-    static_assert(WJ * NW * 1024 == WTILE && XJ * NW * 1024 == XTILE, "whole load blocks");
+    static_assert(WJ * NW * 1024 == WTILE && XBLK * 1024 == XTILE, "whole load blocks");
     static_assert(NST * STAGE * OCC <= 160 * 1024, "LDS");
     static_assert(NST >= 2 && NST <= 4, "ring depth");
     static_assert((NST - 2) * LOADS < 16, "vmcnt immediate");
@@ -188,7 +194,7 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
         const int m = m0 + RPB * (wave + NW * j) + rsub;
-        xv[j] = m < a.M;
+        xv[j] = m < a.M && wave + NW * j < Cf::XBLK;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         xo[j] = (int)(v.n * a.xsn + (long long)v.z * a.sd * a.xsd +
                       (long long)v.p * a.sh * a.xsh + (long long)v.q * a.sw * a.xsw);
@@ -244,8 +250,9 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
 #pragma unroll
         for (int j = 0; j < XJ; ++j) {
             const unsigned ox = (xv[j] && kin) ? (unsigned)(2 * (xo[j] + toff + cc)) : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rx, (LDS_AS void*)(dst + Cf::WTILE + (wave + NW * j) * 1024), 16, (int)ox, 0, 0, 0);
+            const int blk = wave + NW * j;  // past the X tile: zeros into the pad
+            char* xdst = dst + Cf::WTILE + (blk < Cf::XBLK ? blk * 1024 : Cf::XTILE);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (LDS_AS void*)xdst, 16, (int)ox, 0, 0, 0);
         }
         i0 += KB;
         gi += KB;
@@ -406,6 +413,7 @@ const ConvKernel kKernels[] = {
     {4, 32, 128, 2, 6.21, launch_cfg<4, 3, 32, 2>}, {3, 64, 128, 2, 6.18, launch_cfg<3, 2, 64, 2>},
     {2, 64, 128, 2, 6.68, launch_cfg<2, 2, 64, 2>}, {4, 32, 256, 1, 4.78, launch_cfg<4, 4, 32, 4>},
     {3, 64, 256, 1, 5.91, launch_cfg<3, 2, 64, 4>}, {2, 64, 256, 1, 5.47, launch_cfg<2, 3, 64, 4>},
+    {3, 32, 256, 1, 5.55, launch_cfg<3, 4, 32, 4>},
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -425,9 +433,10 @@ int find_kernel(int nb, int kb, int bch) {
 // two per CU: half rounds, a workgroup left alone on its CU at the end
 // counting 1.3 halves), rel and the per-tile term (start-up and epilogue)
 // fitted to six layers on MI355X (VAE decoder 3x3x3 with 128..512 channels,
-// a 1x1x1). GFX906_AMD_CONV_CFG = "<NB>x<KB>" (128 channels) or
-// "<NB>x<KB>x<channels>" (a row of kKernels) overrides the choice (testing);
-// it is read on every call.
+// a 1x1x1; 3x32x256's rel from its ratio to 3x64x256 on one box).
+// GFX906_AMD_CONV_CFG = "<NB>x<KB>" (128 channels) or "<NB>x<KB>x<channels>"
+// (a row of kKernels) overrides the choice (testing); it is read on every
+// call.
 int pick_kernel(long M, int K, long KG) {
     if (const char* e = getenv("GFX906_AMD_CONV_CFG")) {
         int nb = 0, kb = 0, bch = 128;

@@ -60,7 +60,7 @@ def test_reference_cases(i):
     assert got.is_contiguous(memory_format=CL)
 
 
-CFGS = ["4x32", "3x64", "2x64", "4x32x256", "3x64x256", "2x64x256"]  # the launcher's kernels
+CFGS = ["4x32", "3x64", "2x64", "4x32x256", "3x64x256", "2x64x256", "3x32x256"]  # the launcher's kernels
 # C = 24 and 40: several taps per 64-wide k-tile, not a divisor of it
 EXTRA_CASES = [((1, 24, 3, 12, 12), (32, 3, 3, 3), (1, 1, 1), True, False),
                ((1, 40, 4, 10, 14), (48, 3, 3, 3), (1, 1, 1), False, True)]

@@ -176,7 +176,8 @@ def conv_swz(kb, r):
     return (r >> 2) & 3 if kb == 32 else (r >> 1) & 7
 
 
-CONV_KERNELS = [(4, 32, 2), (3, 64, 2), (2, 64, 2), (4, 32, 4), (3, 64, 4), (2, 64, 4)]  # NB, KB, CW
+CONV_KERNELS = [(4, 32, 2), (3, 64, 2), (2, 64, 2), (4, 32, 4), (3, 64, 4), (2, 64, 4),
+                (3, 32, 4)]  # NB, KB, CW
 
 
 @pytest.mark.parametrize("nb,kb,cw", CONV_KERNELS)
@@ -185,8 +186,9 @@ def test_conv3d_load_roles_and_operand_reads(nb, kb, cw):
     rpb = 1024 // rowb
     wtile, xtile = 64 * cw * rowb, 64 * nb * rowb
     for tile_bytes in (wtile, xtile):
-        nblk = tile_bytes // 1024 // nw
-        assert nblk * nw * 1024 == tile_bytes  # whole load blocks per wave
+        tblk = tile_bytes // 1024
+        nblk = -(-tblk // nw)  # loads per wave; past tblk: zeros into the pad
+        assert tile_bytes == wtile and nblk * nw == tblk or tile_bytes == xtile
         seen = {}
         for wave in range(nw):
             for lane in range(64):
@@ -194,6 +196,8 @@ def test_conv3d_load_roles_and_operand_reads(nb, kb, cw):
                 u = (lane % units) ^ conv_swz(kb, rpb * wave + rsub)
                 for j in range(nblk):
                     blk = wave + nw * j
+                    if blk >= tblk:
+                        continue
                     row, slot = rpb * blk + rsub, lane % units
                     assert blk * 1024 + 16 * lane == row * rowb + 16 * slot
                     assert u == slot ^ conv_swz(kb, row)  # same unit in every block j
