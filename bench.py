@@ -96,6 +96,39 @@ def read_profile_figures():
     return out
 
 
+def conv3d_cpu_baseline(x, w, b):
+    """The oracle's implicit GEMM (numpy fp64, oracle/conv3d.py) on the host CPU
+    over one of the layer's six output depth slices (min of 2)."""
+    import numpy as np
+
+    from oracle.conv3d import conv3d_gemm
+
+    xs = x[:, :, 0:3].float().cpu().numpy().astype(np.float16)  # -> one output slice
+    wn, bn = w.float().cpu().numpy().astype(np.float16), b.float().cpu().numpy().astype(np.float16)
+    ts = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        conv3d_gemm(xs, wn, bn)
+        ts.append(time.perf_counter() - t0)
+    t = min(ts)
+    try:  # BLAS threads numpy used
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 0) for i in threadpool_info()
+                       if i.get("user_api") == "blas"), default=0) or os.cpu_count()
+    except Exception:  # noqa: BLE001 - threadpoolctl missing or failing
+        threads = os.cpu_count()
+    k, c, kt, kr, ks = wn.shape
+    m = xs.shape[0] * (xs.shape[2] - kt + 1) * (xs.shape[3] - kr + 1) * (xs.shape[4] - ks + 1)
+    flops = 2 * m * k * c * kt * kr * ks
+    return {
+        "value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle conv3d_gemm (numpy im2col + fp64 GEMM on {threads} BLAS threads) on "
+                   f"output depth slice 1 of 6 ({m} voxels), min of 2: {t:.3f} s; "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
 def conv3d_bench(args):
     """conv3d kernel on a VAE decoder layer: x [1, 512, 8, 64, 64] NDHWC fp16,
     w [512, 512, 3, 3, 3], bias; one JSON line (profiling, not the metric)."""
@@ -148,7 +181,7 @@ def conv3d_bench(args):
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "kernel_ms_avg": round(avg, 4), "kernel_ms_min": round(min(kernel_ms), 4),
                      "algorithmic_flops_per_launch": flops},
-        "cpu_baseline": None}), flush=True)
+        "cpu_baseline": None if args.no_cpu else conv3d_cpu_baseline(x, w, b)}), flush=True)
 
 
 def cpu_baseline():
