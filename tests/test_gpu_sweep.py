@@ -1,0 +1,108 @@
+"""Seeded random sweep of the torch op over shapes, dtypes, scales and
+layouts, against torch SDPA MATH in fp32 on the CPU.
+
+Each case draws (from its own seed) a head dim from every class the kernels
+serve (8..64 padded to the 64 tiles, 128, 512), fp16 or bf16, B and H, ragged
+Sq and Skv, a scale of either sign (0.5 to 1 times D^-0.5), plain or doubled
+q/k (at most as sharp a softmax as the c3 config),
+and a layout per tensor: contiguous, the DiT [B, S, H, D] transpose, a
+padded sequence stride, K/V broadcast over heads, or (D = 512) the VAE's
+token-contiguous K/V view; the output is allocated by the op, or written into
+a [B, S, H, D] or padded view. The bars are those of the other parity tests:
+fp16 max-abs <= 2e-3 and mean-abs <= 2e-4; bf16 eight times that, or the bf16
+rounding of a value within the mean bar where the bf16 spacing alone exceeds
+the max bar.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import gfx906_amd
+from oracle.attention import make_inputs, sdpa_math_fp32, within_tolerance
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+N_CASES = 40
+HEAD_DIMS = [8, 16, 24, 32, 40, 48, 56, 64, 64, 128, 128, 128, 512, 512]
+
+
+def bf16_ok(out, ref):
+    d = (out.float().cpu() - ref).abs()
+    _, e = torch.frexp(ref.abs())
+    half_ulp = torch.ldexp(torch.ones_like(ref), (e - 9).clamp(min=-133))
+    allowed = torch.clamp(half_ulp + 8 * 2e-4, min=8 * 2e-3)
+    return bool((d <= allowed).all()) and d.mean().item() <= 8 * 2e-4, d.max().item(), d.mean().item()
+
+
+def place(x, how, rng):
+    """x [B, H, S, D] on the GPU in layout `how`, same values."""
+    B, H, S, D = x.shape
+    if how == "bshd":
+        buf = torch.empty((B, S, H, D), dtype=x.dtype, device=DEV)
+        v = buf.transpose(1, 2)
+    elif how == "pad":
+        pad = 8 * int(rng.integers(1, 4))
+        v = torch.empty((B, H, S, D + pad), dtype=x.dtype, device=DEV)[..., :D]
+    elif how == "tl":  # [B, D, S] activation seen as [B, 1, S, D] (H == 1)
+        v = torch.empty((B, D, S), dtype=x.dtype, device=DEV).transpose(1, 2).unsqueeze(1)
+    else:
+        v = torch.empty((B, H, S, D), dtype=x.dtype, device=DEV)
+    v.copy_(x.to(DEV))
+    return v
+
+
+def draw_case(i):
+    rng = np.random.default_rng(7000 + i)
+    D = int(rng.choice(HEAD_DIMS))
+    dtype = torch.bfloat16 if rng.random() < 0.3 else torch.float16
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+    smax = 600 if D == 512 else 1200
+    Sq = int(np.exp(rng.uniform(0, np.log(smax))))
+    Skv = int(np.exp(rng.uniform(0, np.log(smax))))
+    # softmax no sharper than the c3 config's (q, k doubled at scale D^-0.5)
+    scale = float(rng.choice([-1, 1]) * rng.uniform(0.5, 1.0) * D ** -0.5)
+    qk_mult = float(rng.choice([1.0, 1.0, 2.0]))
+    lay = [str(rng.choice(["contig", "bshd", "pad"])) for _ in range(4)]
+    if H > 1 and rng.random() < 0.25:
+        lay[1] = lay[2] = "bcast"
+    if D == 512 and rng.random() < 0.5:
+        H = 1
+        Skv = max(8, Skv - Skv % 8)
+        lay[1] = lay[2] = "tl"
+    out_lay = str(rng.choice(["new", "bshd", "pad"]))
+    return dict(D=D, dtype=dtype, B=B, H=H, Sq=Sq, Skv=Skv, scale=scale, qk_mult=qk_mult,
+                lay=lay, out=out_lay, seed=7000 + i, rng=rng)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_case(i):
+    c = draw_case(i)
+    rng = c.pop("rng")
+    print({k: v for k, v in c.items()}, flush=True)
+    B, H, Sq, Skv, D = c["B"], c["H"], c["Sq"], c["Skv"], c["D"]
+    q, k, v = make_inputs(B, H, Sq, Skv, D, c["qk_mult"], 1.0, c["seed"])
+    if c["lay"][1] == "bcast":  # one head of K/V shared by every head
+        k, v = k[:, :1].expand(B, H, Skv, D), v[:, :1].expand(B, H, Skv, D)
+    q, k, v = (t.to(c["dtype"]) for t in (q, k, v))
+    qd = place(q, c["lay"][0], rng)
+    if c["lay"][1] == "bcast":
+        kd = place(k[:, :1], "contig", rng).expand(B, H, Skv, D)
+        vd = place(v[:, :1], "contig", rng).expand(B, H, Skv, D)
+    else:
+        kd, vd = place(k, c["lay"][1], rng), place(v, c["lay"][2], rng)
+    out = None
+    if c["out"] != "new":
+        out = place(torch.zeros(B, H, Sq, D, dtype=c["dtype"]), c["out"], rng)
+    got = gfx906_amd.attn(qd, kd, vd, c["scale"], out=out)
+    torch.cuda.synchronize()
+    if out is not None:
+        assert got.data_ptr() == out.data_ptr()
+    ref = sdpa_math_fp32(q.contiguous(), k.contiguous(), v.contiguous(), c["scale"])
+    if c["dtype"] == torch.float16:
+        ok, mx, mn = within_tolerance(got.float().cpu(), ref)
+    else:
+        ok, mx, mn = bf16_ok(got, ref)
+    print(f"case {i}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    assert ok, (c, mx, mn)
