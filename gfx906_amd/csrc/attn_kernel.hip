@@ -632,11 +632,12 @@ struct Cfg512 {
     static constexpr int DP = 512, NW = 8, BN = 32, BM = NW * 16, NT = NW * 64;
     static constexpr int RB = DP * 2;  // bytes of one K or V row
     // LDS rows are padded instead of swizzled (one direct-load instruction
-    // fills exactly one row, so the padding costs nothing): with a 1040-byte
-    // K stride the QK^T read (16 rows, one 16-byte unit each) and with a
-    // 1056-byte V stride the transposed read (8 rows x 32 bytes per half
-    // wave) touch every bank group once.
-    static constexpr int KS = RB + 16, VS = RB + 32;
+    // fills exactly one row, so the padding costs nothing). A 1056-byte
+    // stride makes both the QK^T read (16 rows, one 16-byte unit each) and
+    // the transposed V read (8 rows x 32 bytes per half wave) free of bank
+    // conflicts on gfx950 (rocprofv3 SQ_LDS_BANK_CONFLICT = 0 for both
+    // patterns; a 1040-byte stride gives the K read 2-way conflicts).
+    static constexpr int KS = RB + 32, VS = RB + 32;
     static constexpr int KTILE = BN * KS, VTILE = BN * VS, STAGE = KTILE + VTILE;
     static constexpr int LDS = 2 * STAGE;
     static constexpr int NLD = BN / NW;  // rows loaded per wave per tile, per tensor
