@@ -645,13 +645,16 @@ struct Cfg512 {
 
 // Token-contiguous layout (k and v with sequence stride 1, the head dim
 // strided: the VAE's [b, c, h*w] activations seen as [b, 1, h*w, c]). A tile
-// arrives as K^T and V^T, 512 dim rows of 32 keys (64 bytes) each, through the
-// same direct loads; 16-byte chunk c of row r sits in slot c ^ tswz(r). The
-// keys of the score blocks are permuted (tkey) so that each lane's P holds 8
-// consecutive keys, making a V^T fragment one 16-byte read, while the
-// transposed K reads of the two 16-lane groups served together fall on
-// complementary 8-byte halves of the slots: both read patterns are free of
-// bank conflicts.
+// arrives as K^T and V^T, 512 dim rows of 32 keys (64 bytes, four 16-byte
+// key chunks) each, through the same direct loads, 1 KB blocks of 16 dim
+// rows. Chunk c of row r sits in slot c ^ tswz(r) of the row in a K^T tile
+// and in slot c ^ vswz512(r) in a V^T tile. The keys of the score blocks are
+// permuted (tkey) so that each lane's P holds 8 consecutive keys, making a
+// V^T fragment one 16-byte read; the transposed K reads of the two 16-lane
+// groups served together fall on complementary 8-byte halves of the slots.
+// Both read patterns measure free of bank conflicts on gfx950 (rocprofv3
+// SQ_LDS_BANK_CONFLICT = 0; the V^T read with the K^T swizzle, or with
+// (r >> 2) & 3, has 2-way conflicts).
 struct Cfg512T {
     static constexpr int ROWB = Cfg512::BN * 2;    // 64 bytes: one dim row of a tile
     static constexpr int TILE = Cfg512::DP * ROWB;  // 32 KB: K^T or V^T of one tile
@@ -660,9 +663,11 @@ struct Cfg512T {
     static constexpr int LPW = TILE / 1024 / Cfg512::NW;  // 1 KB loads per wave, tensor, tile
 };
 
-// Slot swizzle of the token-contiguous tiles: bit 2 of the row to bit 1 of
+// Slot swizzle of the token-contiguous K^T tiles: bit 2 of the row to bit 1 of
 // the slot, bit 3 to bit 0.
 __host__ __device__ constexpr int tswz(int r) { return (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+// Slot swizzle of the token-contiguous V^T tiles.
+__host__ __device__ constexpr int vswz512(int r) { return (r >> 1) & 3; }
 // Key held in row 4j + t of score block kb (j, t < 4) in the token-contiguous
 // kernel: lane group g's rows of blocks 0 and 1 are keys 8g..8g+7.
 __host__ __device__ constexpr int tkey(int kb, int j, int t) { return 8 * j + 4 * ((j + kb) & 1) + t; }
@@ -752,10 +757,12 @@ attn_fwd_d512(const KArgs a) {
     // 8l..8l+7. Rows past Skv read as zeros (the descriptor covers the valid
     // rows only).
     // Token-contiguous layout: lane l of 1 KB block j writes dim row
-    // 16j + l/4, slot l%4, so it fetches key chunk tu = (l%4) ^ tswz(row),
-    // the same in every block; chunks at or past Skv load zeros. Byte offsets
-    // of the lane's rows at key 0 (the host keeps them below 2^31).
+    // 16j + l/4, slot l%4, so it fetches key chunk tu = (l%4) ^ tswz(row) of
+    // K and tv = (l%4) ^ vswz512(row) of V, the same in every block; chunks
+    // at or past Skv load zeros. Byte offsets of the lane's rows at key 0
+    // (the host keeps them below 2^31).
     const int tu = (lane & 3) ^ ((((lane >> 4) & 1) << 1) | ((lane >> 5) & 1));
+    const int tv = (lane & 3) ^ ((lane >> 3) & 3);
     unsigned ktrow[TL ? Cfg512T::LPW : 1], vtrow[TL ? Cfg512T::LPW : 1];
     __amdgpu_buffer_rsrc_t rkt, rvt;
     if constexpr (TL) {
@@ -763,7 +770,7 @@ attn_fwd_d512(const KArgs a) {
         for (int n = 0; n < Cfg512T::LPW; ++n) {
             const long long row = 16 * (wave + n * C::NW) + (lane >> 2);
             ktrow[n] = (unsigned)((row * a.sk.d + 8 * tu) * 2);
-            vtrow[n] = (unsigned)((row * a.sv.d + 8 * tu) * 2);
+            vtrow[n] = (unsigned)((row * a.sv.d + 8 * tv) * 2);
         }
         const int kb = __builtin_amdgcn_readfirstlane((int)(((D - 1) * a.sk.d + Skv) * 2));
         const int vb = __builtin_amdgcn_readfirstlane((int)(((D - 1) * a.sv.d + Skv) * 2));
@@ -773,12 +780,12 @@ attn_fwd_d512(const KArgs a) {
     auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
         if constexpr (TL) {
             const int k0 = t * BN;
-            const bool kin = k0 + 8 * tu < Skv;
+            const bool kin = k0 + 8 * tu < Skv, vin = k0 + 8 * tv < Skv;
 #pragma unroll
             for (int n = 0; n < Cfg512T::LPW; ++n) {
                 const int blk = wave + n * C::NW;
                 const unsigned ok = kin ? ktrow[n] + 2u * (unsigned)k0 : 0xFFFFFFF0u;
-                const unsigned ov = kin ? vtrow[n] + 2u * (unsigned)k0 : 0xFFFFFFF0u;
+                const unsigned ov = vin ? vtrow[n] + 2u * (unsigned)k0 : 0xFFFFFFF0u;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rkt, (LDS_AS void*)(dst + blk * 1024), 16,
                                                          (int)ok, 0, 0, 0);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -831,7 +838,7 @@ attn_fwd_d512(const KArgs a) {
     // of dim row 32s + 8g + 4h + e (chunk j, half (j + kb) & 1; the row's
     // swizzle is tswz = 2h + g%2), so lane i receives key tkey(kb, i/4, i%4),
     // dims 32s + 8g + 4h + 0..3. V^T read: dim row 16ob + i, keys 8g..8g+7
-    // (chunk g), one 16-byte read.
+    // (chunk g), one 16-byte read from slot g ^ vswz512(i).
     int ktb[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -839,7 +846,7 @@ attn_fwd_d512(const KArgs a) {
         for (int kb = 0; kb < 2; ++kb)
             ktb[h][kb] = (8 * g + 4 * h + (i >> 2)) * Cfg512T::ROWB +
                          (((i & 3) ^ ((h << 1) | (g & 1))) * 16) + (((i & 3) + kb) & 1) * 8;
-    const int vtb = i * Cfg512T::ROWB + ((g ^ tswz(i)) * 16);
+    const int vtb = i * Cfg512T::ROWB + ((g ^ vswz512(i)) * 16);
 
     f32x4 oacc[NOB];
 #pragma unroll
