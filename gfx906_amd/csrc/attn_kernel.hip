@@ -100,6 +100,10 @@ struct KArgs {
     int BH, nsplit, split_len;
     float* ws_o;
     float* ws_ml;
+    // Every output row starts 16-byte aligned (o and its batch, head and
+    // sequence strides): the D <= 128 kernels then write O through LDS as
+    // whole 16-byte pieces of consecutive rows.
+    int o16;
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -592,6 +596,45 @@ attn_fwd_pipe(const KArgs a) {
                     }
                 if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[qb], l};
             }
+        }
+        return;
+    }
+    if (!PAD && a.o16) {
+        // O through LDS: each wave writes its rows, in the element type, to a
+        // row-major staging area (rows padded by 16 bytes) in the ring it no
+        // longer reads, then stores them as 16-byte pieces of consecutive
+        // rows. The barrier makes sure every wave is done with the ring.
+        constexpr int RS = DP * 2 + 16;        // staging row stride, bytes
+        constexpr int CPR = DP * 2 / 16;       // 16-byte pieces per row
+        static_assert(2 * 32 * QB * RS <= C::STAGE, "two waves' staging per ring stage");
+        lds_barrier();
+        char* const sa = (wave >> 1) == 0 ? st0 : (wave >> 1) == 1 ? st1 : (wave >> 1) == 2 ? st2 : st3;
+        char* const stg = sa + (wave & 1) * 32 * QB * RS;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float l = half_swap_sum(l_run[qb]);
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+            for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int d0 = 32 * ob + 8 * rr + 4 * g;
+                    const auto h0 = E::cvt2(oacc[qb][ob][4 * rr + 0] * inv,
+                                            oacc[qb][ob][4 * rr + 1] * inv);
+                    const auto h1 = E::cvt2(oacc[qb][ob][4 * rr + 2] * inv,
+                                            oacc[qb][ob][4 * rr + 3] * inv);
+                    *reinterpret_cast<LDS_AS typename E::x4*>(
+                        (LDS_AS char*)stg + (32 * qb + r32) * RS + d0 * 2) =
+                        typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+                }
+        }
+        const int row0 = qrow0 - r32;  // this wave's first row
+#pragma unroll
+        for (int j = 0; j < 32 * QB * CPR / 64; ++j) {
+            const int c = 64 * j + lane, r = c / CPR, col = c - r * CPR;
+            const u32x4 val = *reinterpret_cast<const LDS_AS u32x4*>((const LDS_AS char*)stg +
+                                                                     r * RS + col * 16);
+            if (row0 + r < Sq) *reinterpret_cast<u32x4*>(Oh + (row0 + r) * a.so.s + col * 8) = val;
         }
         return;
     }
@@ -1278,6 +1321,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     a.split_len = 0;
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
+    a.o16 = (uintptr_t)o % 16 == 0 && so.b % 8 == 0 && so.h % 8 == 0 && so.s % 8 == 0 && so.d == 1;
     if (workspace_bytes != (size_t)-1) {  // attn_fwd_split: split the keys if it pays
         const SplitPlan p = plan_split(B, H, Sq, Skv, D);
         const size_t need = split_ws_bytes(p, B, H, Sq, D);
