@@ -34,6 +34,7 @@ PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
 WORKLOAD = dict(B=1, H=16, Sq=16384, Skv=16384, D=128)
 SEED = 106
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_pmc.txt")
+CONV_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3d_vae_kernel_trace.txt")
 
 
 def parse_args():
@@ -81,12 +82,12 @@ def copy_calibration(nbytes, steps):
                       "GB_per_s_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
 
 
-def read_profile_figures():
-    """HBM bytes per launch and counter ratios from the committed summary."""
+def read_profile_figures(path=TRAFFIC_FILE):
+    """HBM bytes per launch and counter ratios from a committed summary."""
     out = {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None}
-    if not os.path.isfile(TRAFFIC_FILE):
+    if not os.path.isfile(path):
         return out
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         text = f.read()
     for key, name in (("traffic", "hbm_bytes_per_launch"), ("mfma_busy_pct", "mfma_busy_pct"),
                       ("lds_bank_conflict_pct", "lds_bank_conflict_pct")):
@@ -179,6 +180,7 @@ def conv3d_bench(args):
         "config": {"workload": "conv3d x[1,512,8,64,64] w[512,512,3,3,3] stride 1, bias"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "traffic": read_profile_figures(CONV_TRAFFIC_FILE)["traffic"],
                      "kernel_ms_avg": round(avg, 4), "kernel_ms_min": round(min(kernel_ms), 4),
                      "algorithmic_flops_per_launch": flops},
         "cpu_baseline": None if args.no_cpu else conv3d_cpu_baseline(x, w, b)}), flush=True)

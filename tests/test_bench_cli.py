@@ -25,3 +25,8 @@ def test_profile_figures_match_the_committed_summary():
     assert fig["traffic"] == 1141170432 + 72034464
     assert f"hbm_bytes_per_launch: {int(fig['traffic'])}" in text
     assert fig["mfma_busy_pct"] == 49.8 and fig["lds_bank_conflict_pct"] == 0.0
+
+
+def test_conv_profile_traffic_is_read():
+    fig = bench.read_profile_figures(bench.CONV_TRAFFIC_FILE)
+    assert fig["traffic"] == 301336832 + 23703552
