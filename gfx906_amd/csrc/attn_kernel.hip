@@ -104,6 +104,11 @@ struct KArgs {
     // sequence strides): the D <= 128 kernels then write O through LDS as
     // whole 16-byte pieces of consecutive rows.
     int o16;
+    // Load Q through LDS, as K (whole rows), in the D = 64 and 128 kernels:
+    // set for q sequence strides up to 2^24 elements and more than 1024 keys
+    // (measured: +1 % north star and c2; with 512 keys the two extra
+    // barriers cost more than the gathered global loads).
+    int q_lds;
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -400,17 +405,22 @@ attn_fwd_pipe(const KArgs a) {
     const int qrow0 = qt * C::BM + wave * 32 * QB + r32;  // this lane's rows: qrow0 + 32 qb
     const int ntiles = (Skv + C::BN - 1) / C::BN;
 
-    // Q^T fragments (B operands), loaded before any tile so that the tile
-    // waits below also cover them.
+    // Q^T fragments (B operands). Through LDS (below) for D = 64 and 128;
+    // else loaded here, before any tile, so that the tile waits below also
+    // cover them.
     x8 qf[QB][NQF];
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
+    const bool q_lds = !PAD && QB == 1 && a.q_lds && ntiles > 0;
+    if (!q_lds) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-        for (int s = 0; s < NQF; ++s) {
-            const int d0 = 16 * s + 8 * g, row = qrow0 + 32 * qb;
-            qf[qb][s] = q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
-        }
+            for (int s = 0; s < NQF; ++s) {
+                const int d0 = 16 * s + 8 * g, row = qrow0 + 32 * qb;
+                qf[qb][s] =
+                    q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
+            }
+    }
 
     f32x16 oacc[QB][NOB];
     float m_run[QB], l_run[QB];
@@ -550,8 +560,38 @@ attn_fwd_pipe(const KArgs a) {
         // Prologue: tiles 0 and 1 in flight, stage 3's V zeroed for the PV
         // of block -1 (P = 0, and 0 * garbage could be NaN), tile 2 issued
         // once tile 0 is in, then S of block 0.
+        // Q through LDS: the workgroup's 256 query rows as four K-shaped
+        // tiles of 64 rows (whole rows per load, the K swizzle) in stages 2
+        // and 3, free until tile 2 is issued; each wave then reads its
+        // fragments with the QK^T read pattern (query row for key row).
+        if (!PAD && QB == 1) {
+            if (q_lds) {
+                static_assert(C::BM == 4 * C::BN, "four Q tiles per workgroup");
+                static_assert(4 * LPT < 16, "vmcnt immediate");
+                int qoff[LPT], qoff_unused[LPT];
+                tile_offsets<C, false>(qoff, qoff_unused, D, (int)a.sq.s, (int)a.sq.s, wave, lane);
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    issue_tile<C>(Qh, qt * C::BM + m * C::BN, Sq, D, a.sq.s,
+                                  (m < 2 ? st2 : st3) + (m & 1) * TILE, wave, qoff);
+            }
+        }
         issue(0, st0);
         issue(1, st1);
+        if (!PAD && QB == 1) {
+            if (q_lds) {
+                __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * LPT));  // this wave's Q loads landed
+                lds_barrier();                                  // every wave's
+                const char* qsrc =
+                    ((wave >> 2) ? st3 : st2) + ((wave >> 1) & 1) * TILE + (wave & 1) * 32 * RB;
+#pragma unroll
+                for (int s = 0; s < NQF; ++s) {
+                    const x8 f = lds_read16<T>(qsrc, kaddr[s & 7] + ((2 * s) & ~15) * 16);
+                    qf[0][s] = __builtin_bit_cast(x8, __builtin_bit_cast(u32x4, f) ^ qneg);
+                }
+                lds_barrier();  // every wave's Q reads are done: stages 2 and 3 are free
+            }
+        }
         for (int i = tid; i < TILE / 16; i += C::NT)
             *reinterpret_cast<u32x4*>(st3 + TILE + 16 * i) = u32x4{};
         __builtin_amdgcn_s_waitcnt(kWaitNext);
@@ -1322,6 +1362,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
     a.o16 = (uintptr_t)o % 16 == 0 && so.b % 8 == 0 && so.h % 8 == 0 && so.s % 8 == 0 && so.d == 1;
+    a.q_lds = sq.s <= (1LL << 24) && Skv > 1024;
     if (workspace_bytes != (size_t)-1) {  // attn_fwd_split: split the keys if it pays
         const SplitPlan p = plan_split(B, H, Sq, Skv, D);
         const size_t need = split_ws_bytes(p, B, H, Sq, D);

@@ -17,6 +17,7 @@ import torch
 
 import gfx906_amd
 from oracle.attention import (CONFIGS, MAX_ABS_TOL, MEAN_ABS_TOL, config_inputs, error_stats,
+                              within_tolerance,
                               make_inputs, sdpa_math_fp32)
 
 pytestmark = pytest.mark.gpu
@@ -321,3 +322,25 @@ def test_runs_on_current_stream():
         out = gfx906_amd.attn(q, k, v, 0.125)
     s.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Sq,scale_sign,q_layout", [(300, 1, "contig"), (1000, -1, "bshd"),
+                                                    (257, 1, "bshd"), (33, -1, "contig")])
+def test_long_key_range_q_through_lds(D, Sq, scale_sign, q_layout):
+    """More than 1024 keys: Q goes through LDS as K-shaped tiles (rows past Sq
+    load zeros, the sign of a negative scale applied after the read, any q
+    sequence stride up to 2^24)."""
+    B, H, Skv = 1, 3, 1500
+    q, k, v = make_inputs(B, H, Sq, Skv, D, seed=D + Sq)
+    scale = scale_sign * D ** -0.5
+    if q_layout == "bshd":
+        qd = torch.empty((B, Sq, H, D), dtype=q.dtype, device=DEV).transpose(1, 2)
+        qd.copy_(q.to(DEV))
+    else:
+        qd = q.to(DEV)
+    out = gfx906_amd.attn(qd, k.to(DEV), v.to(DEV), scale)
+    torch.cuda.synchronize()
+    ok, mx, mn = within_tolerance(out.float().cpu(), sdpa_math_fp32(q, k, v, scale))
+    print(f"D{D} Sq{Sq} {q_layout} sign{scale_sign}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    assert ok, (mx, mn)
