@@ -3,7 +3,9 @@
 // Computes, per (batch, head) and query row i:
 //     o_i = sum_j softmax_j(scale * <q_i, k_j>) * v_j
 // on [B, H, S, D] tensors (any batch / head / sequence strides, unit stride
-// along D) with Sq != Skv allowed, no mask, no dropout. This is the
+// along D; for D = 512 also token-contiguous K and V, unit stride along S)
+// with Sq != Skv allowed, no mask, no dropout; grids too small for the GPU
+// split the key range and merge the partial results. This is the
 // computation behind the reference's `launch` entry point
 // (attn_kernel.hip:710-742, dispatch) and its per-D kernels
 // (attn_pair_gfx906 attn_kernel.hip:313-512 for D=64/128, attn_d512_gfx906
