@@ -646,6 +646,8 @@ attn_fwd_pipe(const KArgs a) {
         // row-major staging area (rows padded by 16 bytes) in the ring it no
         // longer reads, then stores them as 16-byte pieces of consecutive
         // rows. The barrier makes sure every wave is done with the ring.
+        // (These writes are the kernel's only LDS bank conflicts: about 1 %
+        // of its LDS cycles at c2's size; a 32-byte pad measures more.)
         constexpr int RS = DP * 2 + 16;        // staging row stride, bytes
         constexpr int CPR = DP * 2 / 16;       // 16-byte pieces per row
         static_assert(2 * 32 * QB * RS <= C::STAGE, "two waves' staging per ring stage");
