@@ -15,10 +15,12 @@
 // cores:
 //
 //  * Scores are computed transposed, S^T = K * Q^T, with
-//    v_mfma_f32_32x32x16_{f16,bf16}. In the 32x32 accumulator layout a lane
-//    holds one column (one query row) and 16 of the 32 keys of a key block, so
-//    the online-softmax state (running max m, running sum l) is a per-lane
-//    scalar and the row reductions need a single exchange with lane^32.
+//    v_mfma_f32_16x16x32_{f16,bf16} (the card is power-limited under
+//    sustained matrix load, and this form costs less energy per FLOP than
+//    the 32x32x16 one). In the 16x16 accumulator layout a lane holds one
+//    column (one query row) and 4 keys of each 16-key block, so the
+//    online-softmax state is per lane, kept equal over the four lanes that
+//    share a query, and row reductions combine four lanes.
 //  * The same registers, rounded to the input type, are the B operand of
 //    O^T = V^T * P^T. V stays row-major ([key][dim]) in LDS and the A operand
 //    is read with ds_read_b64_tr_b16, whose 16-lane transpose hands each lane
@@ -27,8 +29,8 @@
 //  * K and V tiles go from HBM straight into LDS with buffer loads to LDS
 //    (no VGPR staging), through a ring of four stages, two tiles ahead of
 //    the compute. Rows are XOR-swizzled in 16-byte units so that the QK^T
-//    reads (32 keys x one 16-byte unit) and the transposed V reads (8 keys x
-//    64 bytes) are free of LDS bank conflicts.
+//    reads (16 keys x one 16-byte unit per 16 lanes) and the transposed V
+//    reads (4 keys x 32 bytes per 16 lanes) are free of LDS bank conflicts.
 //  * Each wave is software-pipelined over 32-key blocks: the iteration for
 //    block j issues the PV MFMAs of block j-1 and the QK^T MFMAs of block
 //    j+1 while the VALU turns the scores of block j into P.
@@ -61,7 +63,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -123,9 +124,6 @@ struct Elem<f16> {
     using x8 = f16x8;
     using x4 = f16x4;
     using x2 = f16x2;
-    static __device__ __forceinline__ f32x16 mma32(x8 a, x8 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
     static __device__ __forceinline__ f32x4 mma16(x8 a, x8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
@@ -141,9 +139,6 @@ struct Elem<bf16> {
     using x8 = bf16x8;
     using x4 = bf16x4;
     using x2 = bf16x2;
-    static __device__ __forceinline__ f32x16 mma32(x8 a, x8 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
     static __device__ __forceinline__ f32x4 mma16(x8 a, x8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
@@ -197,18 +192,6 @@ __device__ __forceinline__ typename Elem<T>::x8 lds_read_tr2(const char* base, i
     return __builtin_bit_cast(typename Elem<T>::x8, u32x4{l[0], l[1], h[0], h[1]});
 }
 
-// Max / sum of x over lanes l and l^32 (both halves get the result).
-__device__ __forceinline__ float half_swap_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float half_swap_sum(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                    false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Sum / max over lanes i, i+16, i+32, i+48.
 __device__ __forceinline__ float quad_group_sum(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -236,28 +219,6 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
     return __builtin_bit_cast(typename Elem<T>::x8, __builtin_bit_cast(u32x4, val) ^ qneg);
 }
 
-// P for one 32-key block of S^T (a lane's 16 scores, two 16-key PV steps):
-// p = exp2(s*c + nm) rounded to the element type, nm = -(running max). Adds
-// the block's row-sum contribution, taken from the rounded values, to lsum.
-template <class T>
-__device__ __forceinline__ void block_exp(const f32x16& Sb, typename Elem<T>::x8& P0,
-                                          typename Elem<T>::x8& P1, float nm, float c,
-                                          float& lsum) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        typename Elem<T>::x8& P = h ? P1 : P0;
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e], c, nm));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[8 * h + e + 1], c, nm));
-            const typename Elem<T>::x2 hp = Elem<T>::cvt2(p0, p1);
-            P[e] = hp[0];
-            P[e + 1] = hp[1];
-            lsum = Elem<T>::sum2(hp, lsum);
-        }
-    }
-}
-
 // Whether a block's P needs the exact-max rescale: some lane's row sum over
 // the block exceeds 2^15 or is not finite. Every p <= lsum, so passing the
 // test keeps all p finite in fp16; the first block (running max -1e30,
@@ -268,23 +229,22 @@ __device__ __forceinline__ bool needs_rescale(float lsum) {
 #endif
 
 // XOR swizzles of the 16-byte unit index within a row.
-//  K: the QK^T read takes one unit from 32 consecutive rows, so 16
-//     consecutive rows must land on 16 different bank groups.
-//  V: the transposed read takes 4 units from 8 consecutive rows; each half
-//     wave (4 rows x 4 units) must cover all 16 bank groups.
+//  K: the QK^T read takes one unit from 16 consecutive rows per 16-lane
+//     group, so 16 consecutive rows must land on 16 different bank groups.
+//  V: the transposed read takes 2 units from 4 consecutive rows per 16-lane
+//     group; each half wave (8 rows x 2 units) must cover all 16 bank groups.
 template <int NU>
 __device__ __forceinline__ int kswz(int r) { return NU >= 16 ? (r & 15) : ((r >> 1) & 7); }
 template <int NU>
-__device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+__device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); }
 
 // ---------------------------------------------------------------------------
-// D <= 128: software-pipelined waves, 32 * QB query rows each.
+// D <= 128: software-pipelined waves, 32 query rows each.
 //
 // The iteration for 32-key block j issues the PV MFMAs of block j-1 and the
 // QK^T MFMAs of block j+1 while the VALU turns the scores of block j into P,
 // so every stretch of a wave's instruction stream carries matrix and vector
-// work (two blocks of S and of P are live). With QB = 2 each K or V fragment
-// read from LDS feeds two MFMAs, at twice the accumulator registers.
+// work (two blocks of S and of P are live).
 //
 // K/V tiles are 64 keys (two blocks) in a ring of four LDS stages, separate
 // arrays so that the compiler can tell their accesses apart (a read of one
@@ -296,12 +256,11 @@ __device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 4 * (r & 3) : 4 *
 //
 //   DP  : head dim the tiles are built for (64 or 128; D < 64 is padded)
 //   NW  : waves per workgroup
-//   QB  : 32-row query blocks per wave
 //   OCC : workgroups per CU the register budget is sized for
-template <int DP_, int NW_, int QB_, int OCC_>
+template <int DP_, int NW_, int OCC_>
 struct Cfg {
-    static constexpr int DP = DP_, NW = NW_, QB = QB_, OCC = OCC_, BN = 64;
-    static constexpr int BM = NW * 32 * QB;     // query rows per workgroup
+    static constexpr int DP = DP_, NW = NW_, OCC = OCC_, BN = 64;
+    static constexpr int BM = NW * 32;          // query rows per workgroup
     static constexpr int NT = NW * 64;          // threads per workgroup
     static constexpr int NU = DP / 8;           // 16-byte units per row
     static constexpr int RB = DP * 2;           // bytes per LDS row
@@ -360,20 +319,57 @@ __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int 
 }
 #endif
 
+// MFMA tiling. Every 32x32 block of S^T = K Q^T and of O^T += V^T P^T is
+// computed as four v_mfma_f32_16x16x32 blocks rather than one
+// v_mfma_f32_32x32x16: under sustained matrix load the card is
+// power-limited, and the 16x16x32 form does the same work for less energy
+// (a quarter of the accumulator registers read and written per instruction,
+// for half the FLOPs), so the card holds a higher clock (c2: 2.07 against
+// 1.88 GHz).
+//
+// Per wave: 32 query rows as two 16-column blocks nb. Per 32-key block S^T is
+// 2 (16-key halves kb) x 2 (nb) accumulators; a lane holds, for query
+// 16nb + l%16, keys 16kb + 4(l/16) + 0..3. Those 8 keys, rounded, are the k
+// slots 8(l/16)..+7 of the PV step's B operand, and the transposed V^T read
+// supplies the same key order, so P never leaves registers. A query's keys
+// are spread over four lanes (l%16 + 16j): its running max is kept equal in
+// all four, its row sum is kept per lane and added up at the end.
+//
+// P of one 32-key block for one column block (a lane's 8 scores, keys
+// 4g..4g+3 then 16+4g..): p = exp2(s*c + nm) rounded to the element type,
+// nm = -(running max); adds the row-sum contribution, taken from the rounded
+// values, to lsum.
+#if defined(__HIP_DEVICE_COMPILE__)
+template <class T>
+__device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
+                                            typename Elem<T>::x8& P, float nm, float c,
+                                            float& lsum) {
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const f32x4& Sb = e < 4 ? S0 : S1;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[e & 3], c, nm));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[(e & 3) + 1], c, nm));
+        const typename Elem<T>::x2 hp = Elem<T>::cvt2(p0, p1);
+        P[e] = hp[0];
+        P[e + 1] = hp[1];
+        lsum = Elem<T>::sum2(hp, lsum);
+    }
+}
+#endif
+
 // grid: ceil(Sq / BM) * B*H (* nsplit with SPLIT) workgroups, query tiles of
 // one head adjacent (the splits of one query tile adjacent); block: NW*64
-// threads.
-// The second launch bound is HIP's minimum waves per SIMD (amdgpu_waves_per_eu):
-// OCC workgroups of NW waves over the CU's four SIMDs.
+// threads. The second launch bound is HIP's minimum waves per SIMD
+// (amdgpu_waves_per_eu): OCC workgroups of NW waves over the CU's four SIMDs.
 template <class C, bool PAD, class T, bool SPLIT>
 __global__ void __launch_bounds__(C::NT, C::OCC * C::NW / 4)
 attn_fwd_pipe(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
     using E = Elem<T>;
     using x8 = typename E::x8;
-    constexpr int DP = C::DP, NU = C::NU, RB = C::RB, TILE = C::TILE, QB = C::QB;
-    constexpr int NQF = DP / 16;  // Q fragments (16 dims each) per query block
-    constexpr int NOB = DP / 32;  // 32-dim output blocks
+    constexpr int DP = C::DP, NU = C::NU, RB = C::RB, TILE = C::TILE;
+    constexpr int NQF = DP / 32;          // Q fragments (32 dims each) per column block
+    constexpr int NOB = DP / 16;          // 16-dim output blocks
     constexpr int LPT = C::BLKS / C::NW;  // loads per wave per K (or V) tile
     static_assert(2 * LPT < 16, "vmcnt immediate");
     constexpr int kWaitNext = 0x0F70 | (2 * LPT);  // vmcnt(one tile of loads)
@@ -386,8 +382,7 @@ attn_fwd_pipe(const KArgs a) {
     const float c = a.c;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 5, r32 = lane & 31;
-    const int j16 = lane & 15, G = lane >> 4;
+    const int i = lane & 15, g = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
     int wg = blockIdx.x, split = 0;
     if constexpr (SPLIT) {
@@ -404,36 +399,33 @@ attn_fwd_pipe(const KArgs a) {
     const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h + kv0 * a.sk.s;
     const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h + kv0 * a.sv.s;
     T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
-    const int qrow0 = qt * C::BM + wave * 32 * QB + r32;  // this lane's rows: qrow0 + 32 qb
+    const int qrow0 = qt * C::BM + wave * 32 + i;  // this lane's rows: qrow0 + 16 nb
     const int ntiles = (Skv + C::BN - 1) / C::BN;
 
-    // Q^T fragments (B operands). Through LDS (below) for D = 64 and 128;
-    // else loaded here, before any tile, so that the tile waits below also
-    // cover them.
-    x8 qf[QB][NQF];
+    // Q^T fragments (B operands: column = query 16nb + l%16, k = dims
+    // 32s + 8(l/16)..+7). Through LDS (below) when q_lds is set.
+    x8 qf[2][NQF];
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
-    const bool q_lds = !PAD && QB == 1 && a.q_lds && ntiles > 0;
+    const bool q_lds = !PAD && a.q_lds && ntiles > 0;
     if (!q_lds) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
             for (int s = 0; s < NQF; ++s) {
-                const int d0 = 16 * s + 8 * g, row = qrow0 + 32 * qb;
-                qf[qb][s] =
+                const int d0 = 32 * s + 8 * g, row = qrow0 + 16 * nb;
+                qf[nb][s] =
                     q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
             }
     }
 
-    f32x16 oacc[QB][NOB];
-    float m_run[QB], l_run[QB];
+    f32x4 oacc[NOB][2];
+    float m_run[2], l_run[2];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-        for (int ob = 0; ob < NOB; ++ob) oacc[qb][ob] = f32x16{};
-        // Running max in units of s*c (log2 domain). It starts finite so that
-        // a masked key (score -inf) gives p = 0 rather than NaN.
-        m_run[qb] = -1e30f;
-        l_run[qb] = 0.f;
+        for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] = f32x4{};
+        m_run[nb] = -1e30f;  // finite, so that a masked key (score -inf) gives p = 0
+        l_run[nb] = 0.f;
     }
 
     if (ntiles > 0) {
@@ -443,104 +435,118 @@ attn_fwd_pipe(const KArgs a) {
             issue_tile<C>(Kh, t * C::BN, Skv, D, a.sk.s, dst, wave, koff);
             issue_tile<C>(Vh, t * C::BN, Skv, D, a.sv.s, dst + TILE, wave, voff);
         };
-        int kaddr[8];
+        // K (and Q) read: row 16kb + l%16 of a 32-key block, dims 32s + 8(l/16)..
+        int kaddr[NQF];
         {
-            const int kl = g ^ kswz<NU>(r32);
+            const int kl = kswz<NU>(i);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) kaddr[s] = r32 * RB + (((2 * s) & 15) ^ kl) * 16;
+            for (int s = 0; s < NQF; ++s) kaddr[s] = i * RB + ((4 * s + g) ^ kl) * 16;
         }
-        int vaddr[4];
+        // V^T read (two ds_read_b64_tr_b16): lane 4e + j of group g reads row
+        // 4g + e (+16 for the block's second key half), dims 16ob + 4j..+3, so
+        // lane l receives dim 16ob + l%16 of keys 4g..4g+3 (16 + 4g..).
+        int vaddr[NOB];
         {
-            const int vrow = 4 * g + (j16 >> 2);
-            const int vv = NU >= 16 ? (j16 >> 2) : (j16 >> 3);
-            const int w = 2 * (G & 1) + ((j16 & 3) >> 1);
+            const int vrow = 4 * g + (i >> 2);
+            const int vx = vswz<NU>(vrow) >> 1;
 #pragma unroll
-            for (int ob = 0; ob < 4; ++ob)
-                vaddr[ob] = vrow * RB + (4 * (ob ^ vv) + w) * 16 + 8 * (j16 & 1);
+            for (int ob = 0; ob < NOB; ++ob) vaddr[ob] = vrow * RB + (ob ^ vx) * 32 + (i & 3) * 8;
         }
 
-        // S^T of 32-key block kb of the tile in stage st, every query block.
-        auto qk = [&](const char* st, int kb, f32x16 (&S)[QB]) __attribute__((always_inline)) {
+        // S^T of 32-key block blk of the tile in stage st.
+        auto qk = [&](const char* st, int blk, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) S[qb] = f32x16{};
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int s = 0; s < NQF; ++s) {
-                const x8 kf = lds_read16<T>(st, kaddr[s & 7] + kb * 32 * RB + ((2 * s) & ~15) * 16);
+                for (int nb = 0; nb < 2; ++nb) S[kb][nb] = f32x4{};
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) S[qb] = E::mma32(kf, qf[qb][s], S[qb]);
+            for (int s = 0; s < NQF; ++s)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const x8 kf = lds_read16<T>(st, kaddr[s] + (32 * blk + 16 * kb) * RB);
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) S[kb][nb] = E::mma16(kf, qf[nb][s], S[kb][nb]);
+                }
+            if constexpr (DP == 64) {  // K reads interleaved with the MFMAs (+2 % c5)
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 3, 0);
+#pragma unroll
+                for (int n = 0; n < 2 * NQF - 3; ++n) {
+                    __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
             }
         };
-        // O^T += V^T P^T for 32-key block kb of the tile in stage st.
-        auto pv = [&](const char* st, int kb, const x8 (&P)[QB][2]) __attribute__((always_inline)) {
+        // O^T += V^T P^T for 32-key block blk of the tile in stage st.
+        auto pv = [&](const char* st, int blk, const x8 (&P)[2]) __attribute__((always_inline)) {
             const char* sv = st + TILE;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
+            for (int ob = 0; ob < NOB; ++ob) {
+                const int off = vaddr[ob] + 32 * blk * RB;
+                const x8 vf = lds_read_tr2<T>(sv, off, off + 16 * RB);
 #pragma unroll
-                for (int ob = 0; ob < NOB; ++ob) {
-                    const int off = vaddr[ob & 3] + (2 * kb + ks) * 16 * RB + (ob & ~3) * 64;
-                    const x8 vf = lds_read_tr2<T>(sv, off, off + 8 * RB);
+                for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
+            }
+            // Three V fragments ahead of the MFMAs that use them, then one
+            // more per MFMA pair (measured: +4 % north star against the
+            // compiler's own order).
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 6, 0);
 #pragma unroll
-                    for (int qb = 0; qb < QB; ++qb)
-                        oacc[qb][ob] = E::mma32(vf, P[qb][ks], oacc[qb][ob]);
-                }
+            for (int n = 0; n < NOB - 3; ++n) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
         };
-        // Scores of keys >= Skv (block keys key0..key0+31) to -inf. Taken
-        // for the last one or two blocks only; a branch at the start of an
-        // iteration, so the iteration's MFMAs and VALU work stay in one
-        // scheduling region.
-        auto mask = [&](f32x16 (&S)[QB], int key0) __attribute__((always_inline)) {
+        // Scores of keys >= Skv (block keys key0..key0+31) to -inf, for the
+        // last one or two blocks only.
+        auto mask = [&](f32x4 (&S)[2][2], int key0) __attribute__((always_inline)) {
             if (key0 + 32 > Skv) {
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
-                        if (key >= Skv) S[qb][r] = -INFINITY;
-                    }
+                    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
             }
         };
-        // P of one 32-key block for every query block, with the lazy rescale:
-        // when a row sum fails the test, the exact max of the block's scores
-        // is taken, O and l are rescaled and P is recomputed (a per-wave
-        // branch, so it stays uniform). Any rescale of O comes after the PV
-        // MFMAs issued before this call.
-        auto softmax = [&](f32x16 (&S)[QB], x8 (&P)[QB][2]) __attribute__((always_inline)) {
-            float lp[QB];
+        // P of one 32-key block, with the lazy rescale (a wave-uniform
+        // branch): when some lane's row sum over the block fails the test,
+        // each query takes the exact max of the block over its four lanes,
+        // and O, l and P follow. Any rescale of O comes after the PV MFMAs
+        // issued before this call.
+        auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
+            float lp[2];
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                lp[qb] = 0.f;
-                block_exp<T>(S[qb], P[qb][0], P[qb][1], -m_run[qb], c, lp[qb]);
+            for (int nb = 0; nb < 2; ++nb) {
+                lp[nb] = 0.f;
+                block_exp<T>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
             }
-            float lmax = lp[0];
+            if (__builtin_expect(needs_rescale(fmaxf(lp[0], lp[1])), 0)) {
 #pragma unroll
-            for (int qb = 1; qb < QB; ++qb) lmax = fmaxf(lmax, lp[qb]);
-            if (__builtin_expect(needs_rescale(lmax), 0)) {
+                for (int nb = 0; nb < 2; ++nb) {
+                    float mx = fmaxf(max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]),
+                                     max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]));
+                    mx = quad_group_max(max3(mx, S[1][nb][2], S[1][nb][3])) * c;
+                    const float m_new = fmaxf(m_run[nb], mx);
+                    const float alpha = __builtin_amdgcn_exp2f(m_run[nb] - m_new);
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    float mx = -INFINITY;
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2) mx = max3(mx, S[qb][r], S[qb][r + 1]);
-                    mx = half_swap_max(mx) * c;
-                    const float m_new = fmaxf(m_run[qb], mx);
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-#pragma unroll
-                    for (int ob = 0; ob < NOB; ++ob) oacc[qb][ob] *= alpha;
-                    l_run[qb] *= alpha;
-                    m_run[qb] = m_new;
-                    lp[qb] = 0.f;
-                    block_exp<T>(S[qb], P[qb][0], P[qb][1], -m_new, c, lp[qb]);
+                    for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
+                    l_run[nb] *= alpha;
+                    m_run[nb] = m_new;
+                    lp[nb] = 0.f;
+                    block_exp<T>(S[0][nb], S[1][nb], P[nb], -m_new, c, lp[nb]);
                 }
             }
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) l_run[qb] += lp[qb];
+            for (int nb = 0; nb < 2; ++nb) l_run[nb] += lp[nb];
         };
 
-        f32x16 Sa[QB], Sb[QB];
-        x8 Pa[QB][2], Pb[QB][2];
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) Pb[qb][ks] = x8{};  // block -1: no keys
+        f32x4 Sa[2][2], Sb[2][2];
+        x8 Pa[2], Pb[2];
+        Pb[0] = x8{};  // block -1: no keys
+        Pb[1] = x8{};
 
         // Tile w (blocks 2w, 2w+1) in stage cur; prev holds tile w-1, nxt
         // tile w+1; fill (the stage of tile w-1) takes tile w+3.
@@ -559,19 +565,20 @@ attn_fwd_pipe(const KArgs a) {
             softmax(Sb, Pb);   // block 2w+1
         };
 
-        // Prologue: tiles 0 and 1 in flight, stage 3's V zeroed for the PV
-        // of block -1 (P = 0, and 0 * garbage could be NaN), tile 2 issued
-        // once tile 0 is in, then S of block 0.
-        // Q through LDS: the workgroup's 256 query rows as four K-shaped
-        // tiles of 64 rows (whole rows per load, the K swizzle) in stages 2
-        // and 3, free until tile 2 is issued; each wave then reads its
-        // fragments with the QK^T read pattern (query row for key row).
-        if (!PAD && QB == 1) {
+        // Prologue: tiles 0 and 1 in flight, stage 3's V zeroed for the PV of
+        // block -1 (P = 0, and 0 * garbage could be NaN), tile 2 issued once
+        // tile 0 is in, then S of block 0. Q through LDS: the workgroup's 256
+        // query rows as four K-shaped tiles of 64 rows (whole rows per load,
+        // the K swizzle) in stages 2 and 3, free until tile 2 is issued; each
+        // wave then reads its fragments with the QK^T read pattern (query row
+        // for key row).
+        if constexpr (!PAD) {
             if (q_lds) {
                 static_assert(C::BM == 4 * C::BN, "four Q tiles per workgroup");
                 static_assert(4 * LPT < 16, "vmcnt immediate");
                 int qoff[LPT], qoff_unused[LPT];
-                tile_offsets<C, false>(qoff, qoff_unused, D, (int)a.sq.s, (int)a.sq.s, wave, lane);
+                tile_offsets<C, false>(qoff, qoff_unused, D, (int)a.sq.s, (int)a.sq.s,
+                                             wave, lane);
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
                     issue_tile<C>(Qh, qt * C::BM + m * C::BN, Sq, D, a.sq.s,
@@ -580,31 +587,32 @@ attn_fwd_pipe(const KArgs a) {
         }
         issue(0, st0);
         issue(1, st1);
-        if (!PAD && QB == 1) {
+        if constexpr (!PAD) {
             if (q_lds) {
                 __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * LPT));  // this wave's Q loads landed
                 lds_barrier();                                  // every wave's
                 const char* qsrc =
                     ((wave >> 2) ? st3 : st2) + ((wave >> 1) & 1) * TILE + (wave & 1) * 32 * RB;
 #pragma unroll
-                for (int s = 0; s < NQF; ++s) {
-                    const x8 f = lds_read16<T>(qsrc, kaddr[s & 7] + ((2 * s) & ~15) * 16);
-                    qf[0][s] = __builtin_bit_cast(x8, __builtin_bit_cast(u32x4, f) ^ qneg);
-                }
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int s = 0; s < NQF; ++s) {
+                        const x8 f = lds_read16<T>(qsrc, kaddr[s] + 16 * nb * RB);
+                        qf[nb][s] = __builtin_bit_cast(x8, __builtin_bit_cast(u32x4, f) ^ qneg);
+                    }
                 lds_barrier();  // every wave's Q reads are done: stages 2 and 3 are free
             }
         }
-        for (int i = tid; i < TILE / 16; i += C::NT)
-            *reinterpret_cast<u32x4*>(st3 + TILE + 16 * i) = u32x4{};
+        for (int z = tid; z < TILE / 16; z += C::NT)
+            *reinterpret_cast<u32x4*>(st3 + TILE + 16 * z) = u32x4{};
         __builtin_amdgcn_s_waitcnt(kWaitNext);
         lds_barrier();
         issue(2, st2);
         qk(st0, 0, Sa);
 
-        // Tile w sits in stage w % 4. The loop runs whole groups of four
-        // tiles: tiles past the end hold zeros and are masked to p = 0 (at
-        // most three per workgroup). A single exit keeps the register
-        // allocation of the loop body intact; exits after each tile do not.
+        // Whole groups of four tiles (tiles past the end hold zeros and are
+        // masked to p = 0); a single exit keeps the loop's register
+        // allocation intact.
         for (int w0 = 0;; w0 += 4) {
             tile(w0 + 0, st3, st0, st1, st3);
             tile(w0 + 1, st0, st1, st2, st0);
@@ -620,23 +628,18 @@ attn_fwd_pipe(const KArgs a) {
 
     if constexpr (SPLIT) {  // unnormalised O and (m, l) of this key range
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            const int row = qrow0 + 32 * qb;
-            const float l = half_swap_sum(l_run[qb]);
+        for (int nb = 0; nb < 2; ++nb) {
+            const int row = qrow0 + 16 * nb;
+            const float l = quad_group_sum(l_run[nb]);
             if (row < Sq) {
                 const long long r = ((long long)split * a.BH + bh) * Sq + row;
                 float* wo = a.ws_o + r * D;
 #pragma unroll
-                for (int ob = 0; ob < NOB; ++ob)
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        const int d0 = 32 * ob + 8 * rr + 4 * g;
-                        if (!PAD || d0 < D)
-                            *reinterpret_cast<f32x4*>(wo + d0) =
-                                f32x4{oacc[qb][ob][4 * rr], oacc[qb][ob][4 * rr + 1],
-                                      oacc[qb][ob][4 * rr + 2], oacc[qb][ob][4 * rr + 3]};
-                    }
-                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[qb], l};
+                for (int ob = 0; ob < NOB; ++ob) {
+                    const int d0 = 16 * ob + 4 * g;
+                    if (!PAD || d0 < D) *reinterpret_cast<f32x4*>(wo + d0) = oacc[ob][nb];
+                }
+                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[nb], l};
             }
         }
         return;
@@ -646,36 +649,30 @@ attn_fwd_pipe(const KArgs a) {
         // row-major staging area (rows padded by 16 bytes) in the ring it no
         // longer reads, then stores them as 16-byte pieces of consecutive
         // rows. The barrier makes sure every wave is done with the ring.
-        // (These writes are the kernel's only LDS bank conflicts: about 1 %
-        // of its LDS cycles at c2's size; a 32-byte pad measures more.)
-        constexpr int RS = DP * 2 + 16;        // staging row stride, bytes
-        constexpr int CPR = DP * 2 / 16;       // 16-byte pieces per row
-        static_assert(2 * 32 * QB * RS <= C::STAGE, "two waves' staging per ring stage");
+        constexpr int RS = DP * 2 + 16;   // staging row stride, bytes
+        constexpr int CPR = DP * 2 / 16;  // 16-byte pieces per row
+        static_assert(2 * 32 * RS <= C::STAGE, "two waves' staging per ring stage");
         lds_barrier();
         char* const sa = (wave >> 1) == 0 ? st0 : (wave >> 1) == 1 ? st1 : (wave >> 1) == 2 ? st2 : st3;
-        char* const stg = sa + (wave & 1) * 32 * QB * RS;
+        char* const stg = sa + (wave & 1) * 32 * RS;
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            const float l = half_swap_sum(l_run[qb]);
+        for (int nb = 0; nb < 2; ++nb) {
+            const float l = quad_group_sum(l_run[nb]);
             const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-            for (int ob = 0; ob < NOB; ++ob)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int d0 = 32 * ob + 8 * rr + 4 * g;
-                    const auto h0 = E::cvt2(oacc[qb][ob][4 * rr + 0] * inv,
-                                            oacc[qb][ob][4 * rr + 1] * inv);
-                    const auto h1 = E::cvt2(oacc[qb][ob][4 * rr + 2] * inv,
-                                            oacc[qb][ob][4 * rr + 3] * inv);
-                    *reinterpret_cast<LDS_AS typename E::x4*>(
-                        (LDS_AS char*)stg + (32 * qb + r32) * RS + d0 * 2) =
-                        typename E::x4{h0[0], h0[1], h1[0], h1[1]};
-                }
+            for (int ob = 0; ob < NOB; ++ob) {
+                const int d0 = 16 * ob + 4 * g;
+                const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
+                const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
+                *reinterpret_cast<LDS_AS typename E::x4*>(
+                    (LDS_AS char*)stg + (16 * nb + i) * RS + d0 * 2) =
+                    typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+            }
         }
-        const int row0 = qrow0 - r32;  // this wave's first row
+        const int row0 = qrow0 - i;  // this wave's first row
 #pragma unroll
-        for (int j = 0; j < 32 * QB * CPR / 64; ++j) {
-            const int c = 64 * j + lane, r = c / CPR, col = c - r * CPR;
+        for (int j = 0; j < 32 * CPR / 64; ++j) {
+            const int cidx = 64 * j + lane, r = cidx / CPR, col = cidx - r * CPR;
             const u32x4 val = *reinterpret_cast<const LDS_AS u32x4*>((const LDS_AS char*)stg +
                                                                      r * RS + col * 16);
             if (row0 + r < Sq) *reinterpret_cast<u32x4*>(Oh + (row0 + r) * a.so.s + col * 8) = val;
@@ -683,26 +680,22 @@ attn_fwd_pipe(const KArgs a) {
         return;
     }
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const int row = qrow0 + 32 * qb;
-        const float l = half_swap_sum(l_run[qb]);
+    for (int nb = 0; nb < 2; ++nb) {
+        const int row = qrow0 + 16 * nb;
+        const float l = quad_group_sum(l_run[nb]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         if (row < Sq) {
             T* op = Oh + row * a.so.s;
 #pragma unroll
-            for (int ob = 0; ob < NOB; ++ob)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int d0 = 32 * ob + 8 * rr + 4 * g;
-                    if (!PAD || d0 < D) {
-                        const auto h0 = E::cvt2(oacc[qb][ob][4 * rr + 0] * inv,
-                                                oacc[qb][ob][4 * rr + 1] * inv);
-                        const auto h1 = E::cvt2(oacc[qb][ob][4 * rr + 2] * inv,
-                                                oacc[qb][ob][4 * rr + 3] * inv);
-                        *reinterpret_cast<typename E::x4*>(op + d0) =
-                            typename E::x4{h0[0], h0[1], h1[0], h1[1]};
-                    }
+            for (int ob = 0; ob < NOB; ++ob) {
+                const int d0 = 16 * ob + 4 * g;
+                if (!PAD || d0 < D) {
+                    const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
+                    const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
+                    *reinterpret_cast<typename E::x4*>(op + d0) =
+                        typename E::x4{h0[0], h0[1], h1[0], h1[1]};
                 }
+            }
         }
     }
 #endif
@@ -1140,8 +1133,8 @@ void set_err(const char* msg) {
     g_err[i] = 0;
 }
 
-using Cfg128 = Cfg<128, 8, 1, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
-using Cfg64 = Cfg<64, 8, 1, 2>;    // 64 KB: two workgroups, four waves per SIMD
+using Cfg128 = Cfg<128, 8, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
+using Cfg64 = Cfg<64, 8, 2>;    // 64 KB: two workgroups, four waves per SIMD
 
 template <class T, bool SPLIT>
 void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
