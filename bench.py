@@ -209,9 +209,10 @@ def cpu_baseline():
 
 
 def mfma_ceiling():
-    """Sustained v_mfma_f32_32x32x16_f16 throughput on this GPU (libgfx906_amd_ceiling.so):
+    """Sustained fp16 MFMA throughput on this GPU (libgfx906_amd_ceiling.so):
     the card is power-limited under matrix load, so the clock it holds, and with it the
-    reachable TFLOP/s, depends on how much the operands toggle."""
+    reachable TFLOP/s, depends on how much the operands toggle and on the MFMA shape
+    (v_mfma_f32_32x32x16_f16, and v_mfma_f32_16x16x32_f16 as the attention kernel uses)."""
     import ctypes
 
     from gfx906_amd.build import CEILING_LIB
@@ -223,7 +224,8 @@ def mfma_ceiling():
     lib.mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
     res = {}
-    for mode, name in ((1, "zero_data"), (0, "random_data"), (2, "random_data_attn_valu")):
+    for mode, name in ((1, "zero_data"), (0, "random_data"), (2, "random_data_attn_valu"),
+                       (3, "mfma16_random_data"), (4, "mfma16_random_data_attn_valu")):
         tf, ghz = ctypes.c_double(), ctypes.c_double()
         rc = lib.mfma_ceiling(mode, 4000, 12, ctypes.byref(tf), ctypes.byref(ghz))
         if rc != 0:
@@ -232,8 +234,9 @@ def mfma_ceiling():
                      "frac_of_peak": round(tf.value / PEAK_TFLOPS, 4)}
         print(f"mfma ceiling {name}: {tf.value:.1f} TFLOP/s at {ghz.value:.3f} GHz",
               file=sys.stderr, flush=True)
-    print(json.dumps({"metric": "sustained fp16 MFMA TFLOP/s (v_mfma_f32_32x32x16_f16, "
-                                "2 waves/SIMD, 1 workgroup/CU)",
+    print(json.dumps({"metric": "sustained fp16 MFMA TFLOP/s (v_mfma_f32_32x32x16_f16; "
+                                "mfma16_*: v_mfma_f32_16x16x32_f16; 2 waves/SIMD, "
+                                "1 workgroup/CU)",
                       "unit": "TFLOP/s", "peak": PEAK_TFLOPS, **res}), flush=True)
 
 

@@ -13,6 +13,9 @@
 //   mode 1: all-zero operands (no toggling: the clock stays near 2.4 GHz),
 //   mode 2: mode 0 plus the attention kernel's per-block VALU work (per 16
 //           MFMAs: 16 FMA, 16 exp2, 8 fp32->fp16 pack conversions, 8 dot2),
+//   mode 3: mode 0's work as v_mfma_f32_16x16x32_f16 (two per 32x32x16, the
+//           shape the attention kernel uses),
+//   mode 4: mode 3 plus mode 2's VALU work,
 // and reports TFLOP/s and the average shader clock over the run (s_memtime
 // cycles against the 100 MHz s_memrealtime counter).
 #include <hip/hip_runtime.h>
@@ -23,6 +26,7 @@ typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 512;     // 8 waves: two per SIMD
@@ -61,6 +65,7 @@ mfma_ceiling_kernel(unsigned long long* clk, float* sink, int iters) {
             B[i][e] = MODE == 1 ? (f16)0.f : operand(mix32(t * 977u + i * 29u + e + 7u));
         }
     f32x16 acc[4] = {};
+    f32x4 acc16[8] = {};
     float x[kMfmaPerIter];
 #pragma unroll
     for (int i = 0; i < kMfmaPerIter; ++i) x[i] = (float)(mix32(t + i) & 0xff) * (1.f / 256.f) - 4.f;
@@ -70,9 +75,16 @@ mfma_ceiling_kernel(unsigned long long* clk, float* sink, int iters) {
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int j = 0; j < kMfmaPerIter; ++j) {
-            acc[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 7], B[(j + (j >> 3)) & 7],
-                                                                acc[j & 3], 0, 0, 0);
-            if (MODE == 2) {
+            if (MODE >= 3) {
+                acc16[(2 * j) & 7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    A[j & 7], B[(j + (j >> 3)) & 7], acc16[(2 * j) & 7], 0, 0, 0);
+                acc16[(2 * j + 1) & 7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    A[j & 7], B[(j + (j >> 3) + 3) & 7], acc16[(2 * j + 1) & 7], 0, 0, 0);
+            } else {
+                acc[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 7], B[(j + (j >> 3)) & 7],
+                                                                    acc[j & 3], 0, 0, 0);
+            }
+            if (MODE == 2 || MODE == 4) {
                 const float p = __builtin_amdgcn_exp2f(fmaf(x[j], 0.127f, -1.f));
                 x[j] = p - 0.5f;
                 if (j & 1) {
@@ -87,6 +99,8 @@ mfma_ceiling_kernel(unsigned long long* clk, float* sink, int iters) {
     float s = ls;
 #pragma unroll
     for (int i = 0; i < 4; ++i) s += acc[i][0] + acc[i][15];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += acc16[i][0] + acc16[i][3];
     sink[t] = s;
     if (threadIdx.x == 0) {
         clk[2 * blockIdx.x] = c1 - c0;
@@ -96,12 +110,12 @@ mfma_ceiling_kernel(unsigned long long* clk, float* sink, int iters) {
 
 }  // namespace
 
-// Runs `reps` launches of `iters` loop iterations in mode `mode` (0, 1 or 2,
+// Runs `reps` launches of `iters` loop iterations in mode `mode` (0 to 4,
 // above) on the current device and stream 0; returns the best launch's
 // TFLOP/s (timed with HIP events) and the average shader clock in GHz of the
 // last launch. Returns 0 on success, 1 for bad arguments, 2 on a HIP error.
 extern "C" int mfma_ceiling(int mode, int iters, int reps, double* tflops, double* ghz) {
-    if (mode < 0 || mode > 2 || iters <= 0 || reps <= 0 || !tflops || !ghz) return 1;
+    if (mode < 0 || mode > 4 || iters <= 0 || reps <= 0 || !tflops || !ghz) return 1;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -121,8 +135,12 @@ extern "C" int mfma_ceiling(int mode, int iters, int reps, double* tflops, doubl
             hipLaunchKernelGGL(mfma_ceiling_kernel<0>, dim3(ncu), dim3(kThreads), 0, 0, clk, sink, iters);
         else if (mode == 1)
             hipLaunchKernelGGL(mfma_ceiling_kernel<1>, dim3(ncu), dim3(kThreads), 0, 0, clk, sink, iters);
-        else
+        else if (mode == 2)
             hipLaunchKernelGGL(mfma_ceiling_kernel<2>, dim3(ncu), dim3(kThreads), 0, 0, clk, sink, iters);
+        else if (mode == 3)
+            hipLaunchKernelGGL(mfma_ceiling_kernel<3>, dim3(ncu), dim3(kThreads), 0, 0, clk, sink, iters);
+        else
+            hipLaunchKernelGGL(mfma_ceiling_kernel<4>, dim3(ncu), dim3(kThreads), 0, 0, clk, sink, iters);
         if (hipGetLastError() != hipSuccess) goto done;
         if (hipEventRecord(e1, 0) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) goto done;
         float ms = 0.f;

@@ -217,7 +217,7 @@ def test_mfma_ceiling_library_rejects_bad_arguments_without_launch():
     lib = ctypes.CDLL(str(CEILING_LIB))
     lib.mfma_ceiling.restype = ctypes.c_int
     tf, ghz = ctypes.c_double(), ctypes.c_double()
-    for mode, iters, reps in ((3, 10, 1), (-1, 10, 1), (0, 0, 1), (0, 10, 0)):
+    for mode, iters, reps in ((5, 10, 1), (-1, 10, 1), (0, 0, 1), (0, 10, 0)):
         assert lib.mfma_ceiling(mode, iters, reps, ctypes.byref(tf), ctypes.byref(ghz)) == 1
     assert lib.mfma_ceiling(0, 10, 1, None, ctypes.byref(ghz)) == 1
 

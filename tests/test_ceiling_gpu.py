@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 PEAK = 2516.6
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 def test_ceiling_modes(mode):
     lib = ctypes.CDLL(str(CEILING_LIB))
     lib.mfma_ceiling.restype = ctypes.c_int
