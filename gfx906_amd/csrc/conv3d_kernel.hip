@@ -9,13 +9,16 @@
 //    i = ((t*R + r)*S + s)*C + c the reduction index, so that a packed
 //    channels_last_3d weight row w[k] is contiguous in i and, with C % 8 == 0,
 //    every aligned 8-element group of i lies in one (t, r, s) tap. With W as
-//    the A operand of v_mfma_f32_32x32x16_f16, a lane's accumulator holds
-//    four runs of four consecutive output channels of one voxel: the
+//    the A operand of v_mfma_f32_16x16x32_f16, a lane's accumulator holds a
+//    run of four consecutive output channels of one voxel: the
 //    channels-innermost output, bias and residual move as 8-byte vectors.
+//    (The card is power-limited under sustained matrix load; the 16x16x32
+//    form costs less energy per FLOP than 32x32x16 and holds a higher clock:
+//    +6 % on a VAE decoder layer.)
 //  * Tiles of 64*CW channels x 64*NB voxels x KB reduction elements (CW = 2
 //    or 4, NB = 2, 3 or 4, KB = 32 or 64; seven configurations, chosen per
 //    problem for how the tile count fills the CUs and how long the
-//    reduction is), 2*CW waves of 64 x 32*NB (2 x NB MFMA blocks): with
+//    reduction is), 2*CW waves of 64 x 32*NB (4 x 2NB MFMA blocks): with
 //    CW = 2 two workgroups per CU whose barriers are independent, with
 //    CW = 4 one workgroup of 8 waves that loads fewer bytes per MFMA.
 //    Both operand tiles go from HBM into LDS with buffer loads to LDS (no
@@ -40,7 +43,6 @@ namespace {
 typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_AS __attribute__((address_space(3)))
@@ -72,7 +74,6 @@ struct ConvCfg {
     static constexpr int ROWB = 2 * KB;             // bytes per LDS row
     static constexpr int UNITS = ROWB / 16;         // 16-byte units per row
     static constexpr int RPB = 1024 / ROWB;         // rows per 1 KB load block
-    static constexpr int KSTEPS = KB / 16;          // MFMA k-steps per k-tile
     static constexpr int BVX = 64 * NB;             // output voxels per workgroup
     static constexpr int WTILE = BCH * ROWB;        // bytes of one W tile
     static constexpr int XTILE = BVX * ROWB;        // bytes of one X tile
@@ -155,7 +156,7 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
 #if defined(__HIP_DEVICE_COMPILE__)
     using Cf = ConvCfg<NB, NST, KB, CW>;
     constexpr int STAGE = Cf::STAGE, LOADS = Cf::LOADS, ROWB = Cf::ROWB, UNITS = Cf::UNITS;
-    constexpr int RPB = Cf::RPB, KSTEPS = Cf::KSTEPS, WJ = Cf::WJ, XJ = Cf::XJ, NW = Cf::NW;
+    constexpr int RPB = Cf::RPB, WJ = Cf::WJ, XJ = Cf::XJ, NW = Cf::NW;
     // The ring's stages are separate arrays, so that the compiler can tell
     // their accesses apart: a read of one stage never waits for the loads
     // into another.
@@ -266,30 +267,32 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
         next_tap(wrap);
     };
 
-    // MFMA operand addresses: lane l reads row (32-row block base + l%32),
-    // unit 2*ks + l/32 (16 reduction elements per k-step).
-    const int g = lane >> 5, r32 = lane & 31;
+    // MFMA operand addresses (v_mfma_f32_16x16x32_f16): lane l reads row
+    // (16-row block base + l%16), unit 4*ks + l/16 (32 reduction elements per
+    // k-step).
+    constexpr int KS32 = KB / 32;
+    const int g = lane >> 4, r16 = lane & 15;
     const int wch = wave % CW, wvx = wave / CW;  // channel quarter/half, voxel half
-    int aaddr[2][KSTEPS], baddr[NB][KSTEPS];
+    int aaddr[4][KS32], baddr[2 * NB][KS32];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
+    for (int ks = 0; ks < KS32; ++ks) {
 #pragma unroll
-        for (int bl = 0; bl < 2; ++bl) {
-            const int ra = wch * 64 + bl * 32 + r32;
-            aaddr[bl][ks] = ra * ROWB + (((2 * ks + g) ^ swz<KB>(ra)) * 16);
+        for (int bl = 0; bl < 4; ++bl) {
+            const int ra = wch * 64 + bl * 16 + r16;
+            aaddr[bl][ks] = ra * ROWB + (((4 * ks + g) ^ swz<KB>(ra)) * 16);
         }
 #pragma unroll
-        for (int bl = 0; bl < NB; ++bl) {
-            const int rb = wvx * 32 * NB + bl * 32 + r32;
-            baddr[bl][ks] = Cf::WTILE + rb * ROWB + (((2 * ks + g) ^ swz<KB>(rb)) * 16);
+        for (int bl = 0; bl < 2 * NB; ++bl) {
+            const int rb = wvx * 32 * NB + bl * 16 + r16;
+            baddr[bl][ks] = Cf::WTILE + rb * ROWB + (((4 * ks + g) ^ swz<KB>(rb)) * 16);
         }
     }
 
-    f32x16 acc[2][NB];
+    f32x4 acc[4][2 * NB];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-        for (int vb = 0; vb < NB; ++vb) acc[cb][vb] = f32x16{};
+        for (int vb = 0; vb < 2 * NB; ++vb) acc[cb][vb] = f32x4{};
 
     // One k-tile from stage cur, after issuing the loads of the k-tile NST-1
     // ahead into fill (the stage of the k-tile before this one).
@@ -300,22 +303,25 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
         __builtin_amdgcn_s_waitcnt(0x0F70 | ((NST - 2) * LOADS));
         lds_barrier();    // every wave's; the k-tile in fill was consumed
         issue(fill);
-        f16x8 af[KSTEPS][2], bf[KSTEPS][NB];
+        f16x8 af[KS32][4], bf[KS32][2 * NB];
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
+        for (int ks = 0; ks < KS32; ++ks) {
 #pragma unroll
-            for (int bl = 0; bl < 2; ++bl) af[ks][bl] = lds_read16(cur, aaddr[bl][ks]);
+            for (int bl = 0; bl < 4; ++bl) af[ks][bl] = lds_read16(cur, aaddr[bl][ks]);
 #pragma unroll
-            for (int bl = 0; bl < NB; ++bl) bf[ks][bl] = lds_read16(cur, baddr[bl][ks]);
+            for (int bl = 0; bl < 2 * NB; ++bl) bf[ks][bl] = lds_read16(cur, baddr[bl][ks]);
         }
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
+        for (int ks = 0; ks < KS32; ++ks)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-                for (int vb = 0; vb < NB; ++vb)
-                    acc[cb][vb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks][cb], bf[ks][vb],
+                for (int vb = 0; vb < 2 * NB; ++vb)
+                    acc[cb][vb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks][cb], bf[ks][vb],
                                                                          acc[cb][vb], 0, 0, 0);
+        // With the small-C tap walk, a k-tile's reads hoisted above the
+        // previous k-tile's MFMAs push the wave past 256 VGPRs (spills).
+        if constexpr (SMALLC) __builtin_amdgcn_sched_barrier(0);
     };
     // k-tile t sits in stage t % NST. The loop runs whole groups of NST
     // k-tiles: k-tiles past the end load zeros and add nothing.
@@ -347,27 +353,24 @@ __global__ void __launch_bounds__((ConvCfg<NB, NST, KB, CW>::NT),
     // LDS is released.
     __builtin_amdgcn_s_waitcnt(0x0F70);
 
-    // Epilogue: accumulator row 8(r/4) + 4g + r%4 (an output channel), column
-    // l%32 (an output voxel); four runs of four channels per lane and voxel.
+    // Epilogue: accumulator row 4g + r (an output channel), column l%16 (an
+    // output voxel); one run of four channels per lane, voxel and block.
 #pragma unroll
-    for (int vb = 0; vb < NB; ++vb) {
-        const int m = m0 + wvx * 32 * NB + vb * 32 + r32;
+    for (int vb = 0; vb < 2 * NB; ++vb) {
+        const int m = m0 + wvx * 32 * NB + vb * 16 + r16;
         if (m >= a.M) continue;
         const Voxel v = voxel(m, a.Z, a.P, a.Q);
         const long long oo = v.n * a.osn + v.z * a.osz + v.p * a.osp + v.q * a.osq;
         const long long ro = v.n * a.rsn + v.z * a.rsz + v.p * a.rsp + v.q * a.rsq;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int ch = k0 + wch * 64 + cb * 32 + 8 * rr + 4 * g;
-                if (ch >= a.K) continue;
-                f32x4 val = {acc[cb][vb][4 * rr], acc[cb][vb][4 * rr + 1], acc[cb][vb][4 * rr + 2],
-                             acc[cb][vb][4 * rr + 3]};
-                if (a.bias) val += __builtin_convertvector(*(const f16x4*)(a.bias + ch), f32x4);
-                if (a.res) val += __builtin_convertvector(*(const f16x4*)(a.res + ro + ch), f32x4);
-                *(f16x4*)(a.out + oo + ch) = __builtin_convertvector(val, f16x4);
-            }
+        for (int cb = 0; cb < 4; ++cb) {
+            const int ch = k0 + wch * 64 + cb * 16 + 4 * g;
+            if (ch >= a.K) continue;
+            f32x4 val = acc[cb][vb];
+            if (a.bias) val += __builtin_convertvector(*(const f16x4*)(a.bias + ch), f32x4);
+            if (a.res) val += __builtin_convertvector(*(const f16x4*)(a.res + ro + ch), f32x4);
+            *(f16x4*)(a.out + oo + ch) = __builtin_convertvector(val, f16x4);
+        }
     }
 #endif
 }

@@ -229,13 +229,14 @@ def test_conv3d_load_roles_and_operand_reads(nb, kb, cw):
         # neighbouring lanes fetch whole rows: all units of a row, each once
         for row in range(rows):
             assert sorted(seen[(row, sl)] for sl in range(units)) == list(range(units))
-        # operand reads: row base + l%32, unit 2ks + l/32, 16 lanes served together
-        for base in range(0, rows, 32):
-            for ks in range(kb // 16):
+        # operand reads (v_mfma_f32_16x16x32_f16): row base + l%16, unit
+        # 4ks + l/16, 16 lanes served together
+        for base in range(0, rows, 16):
+            for ks in range(kb // 32):
                 for q in range(4):
                     addrs = []
                     for lane in range(16 * q, 16 * q + 16):
-                        r, unit = base + lane % 32, 2 * ks + lane // 32
+                        r, unit = base + lane % 16, 4 * ks + lane // 16
                         slot = unit ^ conv_swz(kb, r)
                         assert seen[(r, slot)] == unit  # the read finds its unit
                         addrs.append(r * rowb + 16 * slot)
