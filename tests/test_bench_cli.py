@@ -29,4 +29,4 @@ def test_profile_figures_match_the_committed_summary():
 
 def test_conv_profile_traffic_is_read():
     fig = bench.read_profile_figures(bench.CONV_TRAFFIC_FILE)
-    assert fig["traffic"] == 220255744 + 23617536
+    assert fig["traffic"] == 217144832 + 23617536
