@@ -337,13 +337,14 @@ __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int 
 //
 // P of one 32-key block for one column block (a lane's 8 scores, keys
 // 4g..4g+3 then 16+4g..): p = exp2(s*c + nm) rounded to the element type,
-// nm = -(running max); adds the row-sum contribution, taken from the rounded
-// values, to lsum.
+// nm = -(running max). SUM: adds the row-sum contribution, taken from the
+// rounded values, to acc (v_dot2 against 1.0); otherwise folds the largest
+// p into acc (the row sum then comes from an MFMA, below).
 #if defined(__HIP_DEVICE_COMPILE__)
-template <class T>
+template <class T, bool SUM>
 __device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
-                                            typename Elem<T>::x8& P, float nm, float c,
-                                            float& lsum) {
+                                          typename Elem<T>::x8& P, float nm, float c,
+                                          float& acc) {
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
         const f32x4& Sb = e < 4 ? S0 : S1;
@@ -352,7 +353,7 @@ __device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
         const typename Elem<T>::x2 hp = Elem<T>::cvt2(p0, p1);
         P[e] = hp[0];
         P[e + 1] = hp[1];
-        lsum = Elem<T>::sum2(hp, lsum);
+        acc = SUM ? Elem<T>::sum2(hp, acc) : max3(acc, p0, p1);
     }
 }
 #endif
@@ -427,6 +428,17 @@ attn_fwd_pipe(const KArgs a) {
         m_run[nb] = -1e30f;  // finite, so that a masked key (score -inf) gives p = 0
         l_run[nb] = 0.f;
     }
+    // Row sums on the matrix pipe (D = 128): lacc[nb] += A1 * P with A1 = 1
+    // in row 0 and 0 elsewhere, so accumulator row 0 (lane l%16 of lane
+    // group 0) holds the running sum of the rounded p of query 16nb + l%16.
+    // This replaces eight v_dot2 per block, which the matrix pipe cannot
+    // overlap, by two 16x16x32 MFMAs (+1.5 % north star; for D = 64, where
+    // they are 12 % more MFMA work instead of 6 %, it loses 2-3 %).
+    constexpr bool kMfmaSum = DP == 128;
+    f32x4 lacc[2] = {f32x4{}, f32x4{}};
+    x8 aone;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) aone[e] = (T)(i == 0 ? 1.0f : 0.0f);
 
     if (ntiles > 0) {
         int koff[LPT], voff[LPT];
@@ -487,6 +499,9 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
             }
+            if constexpr (kMfmaSum)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
             // Three V fragments ahead of the MFMAs that use them, then one
             // more per MFMA pair (measured: +4 % north star against the
             // compiler's own order).
@@ -512,16 +527,16 @@ attn_fwd_pipe(const KArgs a) {
             }
         };
         // P of one 32-key block, with the lazy rescale (a wave-uniform
-        // branch): when some lane's row sum over the block fails the test,
-        // each query takes the exact max of the block over its four lanes,
-        // and O, l and P follow. Any rescale of O comes after the PV MFMAs
-        // issued before this call.
+        // branch): when some lane's row sum over the block (D = 128: its
+        // largest p) fails the test, each query takes the exact max of the
+        // block over its four lanes, and O, l and P follow. Any rescale of O
+        // comes after the PV MFMAs issued before this call.
         auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
             float lp[2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 lp[nb] = 0.f;
-                block_exp<T>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
+                block_exp<T, !kMfmaSum>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
             }
             if (__builtin_expect(needs_rescale(fmaxf(lp[0], lp[1])), 0)) {
 #pragma unroll
@@ -533,14 +548,18 @@ attn_fwd_pipe(const KArgs a) {
                     const float alpha = __builtin_amdgcn_exp2f(m_run[nb] - m_new);
 #pragma unroll
                     for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-                    l_run[nb] *= alpha;
+                    if constexpr (kMfmaSum)
+                        lacc[nb] *= alpha;
+                    else
+                        l_run[nb] *= alpha;
                     m_run[nb] = m_new;
                     lp[nb] = 0.f;
-                    block_exp<T>(S[0][nb], S[1][nb], P[nb], -m_new, c, lp[nb]);
+                    block_exp<T, !kMfmaSum>(S[0][nb], S[1][nb], P[nb], -m_new, c, lp[nb]);
                 }
             }
+            if constexpr (!kMfmaSum)
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) l_run[nb] += lp[nb];
+                for (int nb = 0; nb < 2; ++nb) l_run[nb] += lp[nb];
         };
 
         f32x4 Sa[2][2], Sb[2][2];
@@ -630,7 +649,7 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int row = qrow0 + 16 * nb;
-            const float l = quad_group_sum(l_run[nb]);
+            const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
             if (row < Sq) {
                 const long long r = ((long long)split * a.BH + bh) * Sq + row;
                 float* wo = a.ws_o + r * D;
@@ -657,7 +676,7 @@ attn_fwd_pipe(const KArgs a) {
         char* const stg = sa + (wave & 1) * 32 * RS;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const float l = quad_group_sum(l_run[nb]);
+            const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
             const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) {
@@ -682,7 +701,7 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         const int row = qrow0 + 16 * nb;
-        const float l = quad_group_sum(l_run[nb]);
+        const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         if (row < Sq) {
             T* op = Oh + row * a.so.s;
