@@ -39,8 +39,10 @@
 //    row sum of p = exp2(s*c - m) exceeds 2^15 (the block's max rose well
 //    above the running max, or this is the first block), which keeps every p
 //    finite in fp16 and skips the rescale on almost every block.
-//  * The row sum l is accumulated from the rounded P (v_dot2_f32_{f16,bf16}
-//    against 1.0), so numerator and denominator see the same rounded weights.
+//  * The row sum l is accumulated from the rounded P, so numerator and
+//    denominator see the same rounded weights: for D = 128 on the matrix pipe
+//    (one more 16x16x32 MFMA per column block, A = a 0/1 row selector), for
+//    D <= 64 with v_dot2_f32_{f16,bf16} against 1.0.
 //  * Output rows are normalised by 1/l and rounded to the input type (RNE),
 //    as the reference does for fp16 (attn_kernel.hip:497-511). Rows of a head
 //    with Skv == 0 are written as zeros (the reference leaves them unwritten).
