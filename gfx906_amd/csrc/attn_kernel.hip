@@ -73,7 +73,8 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 #define LDS_AS __attribute__((address_space(3)))
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Lazy rescale: a block whose lane row sum exceeds this takes the exact max.
+// Lazy rescale: a block whose lane row sum (D = 128: largest p) exceeds this
+// takes the exact max.
 constexpr float kLsumLimit = 32768.0f;
 // Lazy-rescale threshold of the D = 512 kernel: a tile whose largest p
 // exceeds 2^8 takes the exact max.
@@ -221,12 +222,13 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
     return __builtin_bit_cast(typename Elem<T>::x8, __builtin_bit_cast(u32x4, val) ^ qneg);
 }
 
-// Whether a block's P needs the exact-max rescale: some lane's row sum over
-// the block exceeds 2^15 or is not finite. Every p <= lsum, so passing the
+// Whether a block's P needs the exact-max rescale: some lane's bound x
+// (its row sum over the block, or with the row sums on the matrix pipe its
+// largest p) exceeds 2^15 or is not finite. Every p <= x, so passing the
 // test keeps all p finite in fp16; the first block (running max -1e30,
 // p = inf) always fails it.
-__device__ __forceinline__ bool needs_rescale(float lsum) {
-    return __any(!(lsum <= kLsumLimit));
+__device__ __forceinline__ bool needs_rescale(float x) {
+    return __any(!(x <= kLsumLimit));
 }
 #endif
 
