@@ -503,9 +503,7 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
             }
-            if constexpr (kMfmaSum)
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
+
             // Three V fragments ahead of the MFMAs that use them, then one
             // more per MFMA pair (measured: +4 % north star against the
             // compiler's own order).
@@ -564,6 +562,12 @@ attn_fwd_pipe(const KArgs a) {
             if constexpr (!kMfmaSum)
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) l_run[nb] += lp[nb];
+            // Row sums of this block's P (D = 128): issued here, where the
+            // wave's stream is mostly VALU work (+0.6 % north star against
+            // issuing them with the PV MFMAs), after any rescale of lacc.
+            if constexpr (kMfmaSum)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
         };
 
         f32x4 Sa[2][2], Sb[2][2];
