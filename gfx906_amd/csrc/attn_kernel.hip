@@ -35,10 +35,12 @@
 //    block j issues the PV MFMAs of block j-1 and the QK^T MFMAs of block
 //    j+1 while the VALU turns the scores of block j into P.
 //  * Softmax runs in fp32 with exp2 and scale*log2(e) folded into one FMA.
-//    The running max is updated lazily: O is rescaled only when a block's
-//    row sum of p = exp2(s*c - m) exceeds 2^15 (the block's max rose well
-//    above the running max, or this is the first block), which keeps every p
-//    finite in fp16 and skips the rescale on almost every block.
+//    P = exp2(s*c - m) is computed with the running max m and tested: when
+//    some rounded p exceeds a limit, the block's exact max is taken and O,
+//    l and P follow (a wave-uniform branch). D = 128 updates m lazily
+//    (limit 2^15: every p stays finite in fp16, and the rescale is skipped
+//    on almost every block); D <= 64 keeps the exact running max (limit 1:
+//    a row's dominant weight is exactly 1.0); D = 512 uses limit 2^8.
 //  * The row sum l is accumulated from the rounded P, so numerator and
 //    denominator see the same rounded weights: for D = 128 on the matrix pipe
 //    (one more 16x16x32 MFMA per column block, A = a 0/1 row selector), for
@@ -73,9 +75,9 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 #define LDS_AS __attribute__((address_space(3)))
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Lazy rescale: a block whose lane row sum (D = 128: largest p) exceeds this
-// takes the exact max.
-constexpr float kLsumLimit = 32768.0f;
+// Lazy rescale of the D = 128 kernel: a block with some p above this takes
+// the exact max.
+constexpr float kPLazyLimit = 32768.0f;
 // Lazy-rescale threshold of the D = 512 kernel: a tile whose largest p
 // exceeds 2^8 takes the exact max.
 constexpr float kPmaxLimit = 256.0f;
@@ -159,21 +161,28 @@ __device__ __forceinline__ typename Elem<T>::x8 ld_global16(const T* p) {
     return *reinterpret_cast<const typename Elem<T>::x8*>(p);
 }
 
-// Three-way max; with NaN-free arithmetic assumed (-fno-honor-nans) the
-// backend selects v_max3_f32 for it.
 // Workgroup barrier for the LDS ring: this wave's LDS reads and writes are
 // complete (lgkmcnt(0)), then s_barrier. __syncthreads() would add a release
 // fence that also waits for every load to LDS still in flight (vmcnt(0)),
 // which drains the tiles meant to stay in flight across the barrier. Each
 // wave first waits for its own part of the tile it needs (vmcnt(n)); the
-// barrier then orders every wave's part before the reads that follow.
+// barrier then orders every wave's part before the reads that follow. The
+// memory clobber keeps the compiler from moving LDS accesses across it
+// (the s_waitcnt and s_barrier builtins alone are not memory operations to
+// the optimiser).
 __device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Three-way max. fmaxf in the default IEEE mode quiets its operands first
+// (a v_max_f32 x, x, x per operand not known to come from arithmetic, e.g.
+// MFMA results); the IEEE 754-2019 maximum propagates NaN instead and maps
+// to gfx950's v_maximum3_f32 with no such step.
 __device__ __forceinline__ float max3(float a, float b, float c) {
-    return fmaxf(fmaxf(a, b), c);
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+__device__ __forceinline__ float max2(float a, float b) {
+    return __builtin_elementwise_maximum(a, b);
 }
 
 // 16-byte LDS read at a byte address.
@@ -207,10 +216,10 @@ __device__ __forceinline__ float quad_group_sum(float x) {
 __device__ __forceinline__ float quad_group_max(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                     false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max2(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                     false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max2(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Q^T fragment: 8 elements of a query row with the sign flipped for a
@@ -222,13 +231,32 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
     return __builtin_bit_cast(typename Elem<T>::x8, __builtin_bit_cast(u32x4, val) ^ qneg);
 }
 
-// Whether a block's P needs the exact-max rescale: some lane's bound x
-// (its row sum over the block, or with the row sums on the matrix pipe its
-// largest p) exceeds 2^15 or is not finite. Every p <= x, so passing the
-// test keeps all p finite in fp16; the first block (running max -1e30,
-// p = inf) always fails it.
-__device__ __forceinline__ bool needs_rescale(float x) {
-    return __any(!(x <= kLsumLimit));
+// Whether some element of a block's rounded P (two 8-element operands, all
+// non-negative) exceeds `lim` or is NaN, in any lane of the wave. The first
+// block (running max -1e30, p = inf) always does. fp16: a tree of
+// v_pk_maximum3_f16 over the eight packed registers. bf16 (no packed bf16
+// maximum): non-negative bf16 values order as their 16-bit patterns, so a
+// tree of packed unsigned 16-bit maxima (NaN patterns sort above inf).
+template <class T>
+__device__ __forceinline__ bool p_above(const typename Elem<T>::x8 (&P)[2], float lim) {
+    const u32x4 a = __builtin_bit_cast(u32x4, P[0]), b = __builtin_bit_cast(u32x4, P[1]);
+    if constexpr (std::is_same<T, f16>::value) {
+        auto h = [](unsigned u) { return __builtin_bit_cast(f16x2, u); };
+        auto mx = [](f16x2 x, f16x2 y) { return __builtin_elementwise_maximum(x, y); };
+        const f16x2 x = mx(mx(h(a[0]), h(a[1])), h(a[2]));
+        const f16x2 y = mx(mx(h(a[3]), h(b[0])), h(b[1]));
+        const f16x2 z = mx(mx(h(b[2]), h(b[3])), x);
+        const f16x2 r = mx(y, z);
+        return __any(!(r[0] <= (f16)lim) || !(r[1] <= (f16)lim));
+    } else {
+        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+        auto u = [](unsigned w) { return __builtin_bit_cast(u16x2, w); };
+        auto mx = [](u16x2 x, u16x2 y) { return __builtin_elementwise_max(x, y); };
+        const u16x2 r = mx(mx(mx(u(a[0]), u(a[1])), mx(u(a[2]), u(a[3]))),
+                           mx(mx(u(b[0]), u(b[1])), mx(u(b[2]), u(b[3]))));
+        const unsigned short lb = __builtin_bit_cast(unsigned short, (bf16)lim);
+        return __any(max(r[0], r[1]) > lb);
+    }
 }
 #endif
 
@@ -342,8 +370,8 @@ __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int 
 // P of one 32-key block for one column block (a lane's 8 scores, keys
 // 4g..4g+3 then 16+4g..): p = exp2(s*c + nm) rounded to the element type,
 // nm = -(running max). SUM: adds the row-sum contribution, taken from the
-// rounded values, to acc (v_dot2 against 1.0); otherwise folds the largest
-// p into acc (the row sum then comes from an MFMA, below).
+// rounded values, to acc (v_dot2 against 1.0); otherwise the row sum comes
+// from an MFMA (below).
 #if defined(__HIP_DEVICE_COMPILE__)
 template <class T, bool SUM>
 __device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
@@ -357,7 +385,7 @@ __device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
         const typename Elem<T>::x2 hp = Elem<T>::cvt2(p0, p1);
         P[e] = hp[0];
         P[e + 1] = hp[1];
-        acc = SUM ? Elem<T>::sum2(hp, acc) : max3(acc, p0, p1);
+        if constexpr (SUM) acc = Elem<T>::sum2(hp, acc);
     }
 }
 #endif
@@ -424,14 +452,6 @@ attn_fwd_pipe(const KArgs a) {
     }
 
     f32x4 oacc[NOB][2];
-    float m_run[2], l_run[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] = f32x4{};
-        m_run[nb] = -1e30f;  // finite, so that a masked key (score -inf) gives p = 0
-        l_run[nb] = 0.f;
-    }
     // Row sums on the matrix pipe (D = 128): lacc[nb] += A1 * P with A1 = 1
     // in row 0 and 0 elsewhere, so accumulator row 0 (lane l%16 of lane
     // group 0) holds the running sum of the rounded p of query 16nb + l%16.
@@ -439,6 +459,24 @@ attn_fwd_pipe(const KArgs a) {
     // overlap, by two 16x16x32 MFMAs (+1.5 % north star; for D = 64, where
     // they are 12 % more MFMA work instead of 6 %, it loses 2-3 %).
     constexpr bool kMfmaSum = DP == 128;
+    // Running max of each query column block. D = 128 keeps a lazy one, in
+    // log2 units (s*c), raised only when some p exceeds 2^15 (rare after the
+    // first blocks: every p stays finite in fp16); it starts at -1e30
+    // (finite, so that a masked key, score -inf, gives p = 0). D <= 64 keeps
+    // the exact running max, in score units (s), starting at -inf (the first
+    // block's scores always exceed it), so that the dominant weight of a
+    // row is exactly 1.0 in fp16: with a stale max it carries a rounding
+    // error of up to 2^-11 relative, which on sharp rows with |o| near 4 and
+    // above (c3: q, k ~ 2 N(0,1), 512 keys) moves the output past the 2e-3
+    // bar.
+    float m_run[2], l_run[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] = f32x4{};
+        m_run[nb] = kMfmaSum ? -1e30f : -INFINITY;
+        l_run[nb] = 0.f;
+    }
     f32x4 lacc[2] = {f32x4{}, f32x4{}};
     x8 aone;
 #pragma unroll
@@ -528,46 +566,68 @@ attn_fwd_pipe(const KArgs a) {
                             if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
             }
         };
-        // P of one 32-key block, with the lazy rescale (a wave-uniform
-        // branch): when some lane's row sum over the block (D = 128: its
-        // largest p) fails the test, each query takes the exact max of the
-        // block over its four lanes, and O, l and P follow. Any rescale of O
-        // comes after the PV MFMAs issued before this call.
-        auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
-            float lp[2];
+        // O, l and m of column block nb move to the running max m_new
+        // (m_run's units).
+        auto rescale = [&](int nb, float m_new) __attribute__((always_inline)) {
+            const float alpha =
+                __builtin_amdgcn_exp2f(kMfmaSum ? m_run[nb] - m_new : (m_run[nb] - m_new) * c);
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                lp[nb] = 0.f;
-                block_exp<T, !kMfmaSum>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
-            }
-            if (__builtin_expect(needs_rescale(fmaxf(lp[0], lp[1])), 0)) {
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    float mx = fmaxf(max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]),
-                                     max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]));
-                    mx = quad_group_max(max3(mx, S[1][nb][2], S[1][nb][3])) * c;
-                    const float m_new = fmaxf(m_run[nb], mx);
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[nb] - m_new);
-#pragma unroll
-                    for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-                    if constexpr (kMfmaSum)
-                        lacc[nb] *= alpha;
-                    else
-                        l_run[nb] *= alpha;
-                    m_run[nb] = m_new;
-                    lp[nb] = 0.f;
-                    block_exp<T, !kMfmaSum>(S[0][nb], S[1][nb], P[nb], -m_new, c, lp[nb]);
-                }
-            }
-            if constexpr (!kMfmaSum)
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) l_run[nb] += lp[nb];
-            // Row sums of this block's P (D = 128): issued here, where the
-            // wave's stream is mostly VALU work (+0.6 % north star against
-            // issuing them with the PV MFMAs), after any rescale of lacc.
+            for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
             if constexpr (kMfmaSum)
+                lacc[nb] *= alpha;
+            else
+                l_run[nb] *= alpha;
+            m_run[nb] = m_new;
+        };
+        auto lane_max = [&](const f32x4 (&S)[2][2], int nb) __attribute__((always_inline)) {
+            const float mx = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
+            const float my = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
+            return max2(max3(mx, S[1][nb][2], S[1][nb][3]), my);
+        };
+        // P of one 32-key block. Any rescale of O comes after the PV MFMAs
+        // issued before this call.
+        //  D = 128 (lazy max): P is computed with the running max first and
+        //  tested; when some rounded p exceeds 2^15 (rare after the first
+        //  blocks) each query takes its exact block max and O, l and P follow
+        //  (a wave-uniform branch).
+        //  D <= 64 (exact running max, in score units): the lane's largest
+        //  score is compared with the running max before any exponential;
+        //  when some query's block max rises above it, the queries take their
+        //  exact block max and O and l are rescaled, then P is computed once.
+        //  Maxima rise often on short key ranges (most blocks of c3), where
+        //  computing P first would compute it twice. A dominant key then
+        //  gives p = exp2(fma(s, c, -RN(s*c))), within 2^-20 of 1, which
+        //  rounds to exactly 1.0.
+        auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
+            if constexpr (kMfmaSum) {
+                float lp[2];  // unused: the row sums come from the MFMAs below
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
+                if (__builtin_expect(p_above<T>(P, kPLazyLimit), 0)) {
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        rescale(nb, max2(m_run[nb], quad_group_max(lane_max(S, nb)) * c));
+                        block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
+                    }
+                }
+                // Row sums of this block's P: issued here, where the wave's
+                // stream is mostly VALU work (+0.6 % north star against
+                // issuing them with the PV MFMAs), after any rescale of lacc.
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
+            } else {
+                const float lm0 = lane_max(S, 0), lm1 = lane_max(S, 1);
+                if (__any(lm0 > m_run[0] || lm1 > m_run[1])) {
+                    const float lm[2] = {lm0, lm1};
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        rescale(nb, max2(m_run[nb], quad_group_max(lm[nb])));
+                }
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    block_exp<T, true>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, l_run[nb]);
+            }
         };
 
         f32x4 Sa[2][2], Sb[2][2];
@@ -666,7 +726,8 @@ attn_fwd_pipe(const KArgs a) {
                     const int d0 = 16 * ob + 4 * g;
                     if (!PAD || d0 < D) *reinterpret_cast<f32x4*>(wo + d0) = oacc[ob][nb];
                 }
-                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[nb], l};
+                const float m = kMfmaSum ? m_run[nb] : m_run[nb] * c;  // log2 units
+                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m, l};
             }
         }
         return;
@@ -1292,7 +1353,11 @@ int check_args(const void* q, const void* k, const void* v, void* o, int B, int 
         return fail("attn: head_dim must be <=64 and a multiple of 8, or 128, or 512");
     if (dtype != ATTN_DTYPE_F16 && dtype != ATTN_DTYPE_BF16)
         return fail("attn: dtype must be ATTN_DTYPE_F16 or ATTN_DTYPE_BF16");
-    if ((long)B * H * ((Sq + 31) / 32) > 0x7fffffffL || (long)B * H > 65535)
+    // One workgroup per (batch, head, query tile) in grid.x; HIP bounds
+    // grid.x * block size by 2^32 (512 threads per workgroup; query tiles
+    // of 128 rows for D = 512, 256 otherwise).
+    if ((long long)B * H * ((Sq + (D == 512 ? 127 : 255)) / (D == 512 ? 128 : 256)) * 512 >=
+        (1LL << 32))
         return fail("attn: grid too large");
     if (B == 0 || H == 0 || Sq == 0) return 0;
     if (!q || !o || (Skv > 0 && (!k || !v))) return fail("attn: null pointer");

@@ -108,10 +108,10 @@ __host__ __device__ constexpr int swz(int r) { return KB == 32 ? (r >> 2) & 3 : 
 // complete (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() there is no
 // release fence: that fence also waits for every outstanding load to LDS
 // (vmcnt(0)), including the k-tiles meant to stay in flight. Each wave waits
-// for its own part of the k-tile to be read (vmcnt(n)) before this.
+// for its own part of the k-tile to be read (vmcnt(n)) before this. The
+// memory clobber keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ f16x8 lds_read16(const char* base, int byte_off) {

@@ -70,6 +70,19 @@ def test_negative_sizes_and_null_pointers_rejected():
     assert b"null" in lib.attn_last_error()
 
 
+def test_many_batch_heads_are_not_a_grid_limit():
+    # B*H above 65535 reaches the pointer checks (no "grid too large"): the
+    # grid is one-dimensional and only HIP's 2^32 work-item bound applies.
+    lib = gfx906_amd.capi()
+    assert lib.attn_fwd(None, None, None, None, 65536, 1, 8, 8, 8, 0.1, None) == 1
+    assert b"null" in lib.attn_last_error()
+    assert lib.attn_fwd(None, None, None, None, 2, 40000, 3, 5, 64, 0.1, None) == 1
+    assert b"null" in lib.attn_last_error()
+    # 2^23 query tiles of 512 threads reach 2^32 work items.
+    assert lib.attn_fwd(None, None, None, None, 1 << 14, 1 << 9, 256, 8, 64, 0.1, None) == 1
+    assert b"grid too large" in lib.attn_last_error()
+
+
 def test_empty_problem_is_a_no_op():
     lib = gfx906_amd.capi()
     assert lib.attn_fwd(None, None, None, None, 0, 4, 4, 4, 64, 0.1, None) == 0
