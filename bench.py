@@ -10,9 +10,10 @@ resident in HBM. Prints one JSON line with the driver's fields plus:
   on the stream the kernel runs on, against MI355X's dense fp16 MFMA peak;
   ``traffic`` is the HBM bytes per launch read from the committed rocprofv3
   counter summary (profiles/), or null when that file is absent.
-* ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine) on
-  a bounded sample of the same workload: two heads, all query rows against
-  all keys, chunked by 2048 query rows.
+* ``counters``: MFMA busy % and LDS bank-conflict % from the committed
+  rocprofv3 summary, with the workload they were measured on.
+* ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine)
+  over the whole workload, chunked by head and 2048 query rows.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -50,10 +51,6 @@ def parse_args():
                          "kernel on a 512->512 3x3x3 VAE layer)")
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
                     help="attention input type (profiling; the metric is quoted for fp16)")
-    ap.add_argument("--ceiling", action="store_true",
-                    help="instead of attention, measure the sustained fp16 MFMA throughput and "
-                         "shader clock of this GPU on random data, zero data, and random data "
-                         "with the attention kernel's VALU mix (one JSON line)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="instead of attention, time a plain device copy of this many bytes "
                          "(reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -83,8 +80,10 @@ def copy_calibration(nbytes, steps):
 
 
 def read_profile_figures(path=TRAFFIC_FILE):
-    """HBM bytes per launch and counter ratios from a committed summary."""
-    out = {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None}
+    """HBM bytes per launch, counter ratios and the workload the counters were
+    measured on, from a committed summary's "name: value" lines."""
+    out = {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None,
+           "counters_workload": None}
     if not os.path.isfile(path):
         return out
     with open(path) as f:
@@ -94,6 +93,9 @@ def read_profile_figures(path=TRAFFIC_FILE):
         m = re.search(rf"^{name}\s*[:=]\s*([0-9.eE+-]+)", text, re.M)
         if m:
             out[key] = float(m.group(1))
+    m = re.search(r"^counters_workload\s*[:=]\s*(.+)$", text, re.M)
+    if m:
+        out["counters_workload"] = m.group(1).strip()
     return out
 
 
@@ -148,7 +150,7 @@ def conv3d_bench(args):
     out = torch.empty(n, k, z, p, q, dtype=torch.float16, device="cuda").contiguous(
         memory_format=cl)
     dims = [n, d, h, wd, c, k, t, t, t, 1, 1, 1, z, p, q]
-    xs, os_ = list(kitchen._packed_strides(x.shape)), list(kitchen._packed_strides(out.shape))
+    xs, os_ = list(kitchen.packed_strides(x.shape)), list(kitchen.packed_strides(out.shape))
     conv = gfx906_amd.extension().conv3d
 
     def call():
@@ -187,57 +189,34 @@ def conv3d_bench(args):
 
 
 def cpu_baseline():
-    """torch SDPA MATH on CPU, fp32 upcast, 2 heads of the workload (min of 3)."""
+    """torch SDPA MATH on the host CPU (fp32 upcast of the same fp16 inputs,
+    the oracle's routine) over the whole workload: every head and query row,
+    chunked per head and by 2048 query rows (chunk times summed); one warm-up
+    chunk, then the best of 2 full passes."""
     import torch
 
-    from oracle.attention import make_inputs, time_cpu_sdpa
+    from oracle.attention import chunked_sdpa_math, make_inputs
 
     w = WORKLOAD
-    heads = 2
-    q, k, v = make_inputs(1, heads, w["Sq"], w["Skv"], w["D"], seed=SEED)
-    t = time_cpu_sdpa(q, k, v, w["D"] ** -0.5, reps=3)
-    flops = 4 * heads * w["Sq"] * w["Skv"] * w["D"]
+    q, k, v = make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"], seed=SEED)
+    scale = w["D"] ** -0.5
+    chunked_sdpa_math(q[:, :1, :2048], k[:, :1], v[:, :1], scale)  # warm-up
+    best = float("inf")
+    for _ in range(2):
+        t0 = time.perf_counter()
+        chunked_sdpa_math(q, k, v, scale)
+        best = min(best, time.perf_counter() - t0)
+    flops = 4 * w["B"] * w["H"] * w["Sq"] * w["Skv"] * w["D"]
     return {
-        "value": round(flops / t / 1e12, 4),
+        "value": round(flops / best / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"torch SDPA MATH (fp32 upcast) on CPU, {heads} of {w['H']} heads, "
-                   f"Sq=Skv={w['Sq']}, D={w['D']}, chunked by 2048 query rows, min of 3 "
-                   f"after 1 warm-up: {t:.3f} s; os.cpu_count()={os.cpu_count()}"),
+        "sample": (f"torch SDPA MATH (fp32 upcast) on CPU over the whole workload: all "
+                   f"{w['H']} heads, Sq=Skv={w['Sq']}, D={w['D']}, chunked by 2048 query rows "
+                   f"(times summed), best of 2 passes after a warm-up chunk: {best:.2f} s; "
+                   f"os.cpu_count()={os.cpu_count()}"),
     }
-
-
-def mfma_ceiling():
-    """Sustained fp16 MFMA throughput on this GPU (libgfx906_amd_ceiling.so):
-    the card is power-limited under matrix load, so the clock it holds, and with it the
-    reachable TFLOP/s, depends on how much the operands toggle and on the MFMA shape
-    (v_mfma_f32_32x32x16_f16, and v_mfma_f32_16x16x32_f16 as the attention kernel uses)."""
-    import ctypes
-
-    from gfx906_amd.build import CEILING_LIB
-
-    if not CEILING_LIB.is_file():
-        raise RuntimeError(f"{CEILING_LIB} not built; run python -m gfx906_amd.build")
-    lib = ctypes.CDLL(str(CEILING_LIB))
-    lib.mfma_ceiling.restype = ctypes.c_int
-    lib.mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
-    res = {}
-    for mode, name in ((1, "zero_data"), (0, "random_data"), (2, "random_data_attn_valu"),
-                       (3, "mfma16_random_data"), (4, "mfma16_random_data_attn_valu")):
-        tf, ghz = ctypes.c_double(), ctypes.c_double()
-        rc = lib.mfma_ceiling(mode, 4000, 12, ctypes.byref(tf), ctypes.byref(ghz))
-        if rc != 0:
-            raise RuntimeError(f"mfma_ceiling mode {mode} failed with status {rc}")
-        res[name] = {"tflops": round(tf.value, 1), "clock_ghz": round(ghz.value, 3),
-                     "frac_of_peak": round(tf.value / PEAK_TFLOPS, 4)}
-        print(f"mfma ceiling {name}: {tf.value:.1f} TFLOP/s at {ghz.value:.3f} GHz",
-              file=sys.stderr, flush=True)
-    print(json.dumps({"metric": "sustained fp16 MFMA TFLOP/s (v_mfma_f32_32x32x16_f16; "
-                                "mfma16_*: v_mfma_f32_16x16x32_f16; 2 waves/SIMD, "
-                                "1 workgroup/CU)",
-                      "unit": "TFLOP/s", "peak": PEAK_TFLOPS, **res}), flush=True)
 
 
 def main():
@@ -256,9 +235,6 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.steps)
-        return
-    if args.ceiling:
-        mfma_ceiling()
         return
 
     if args.workload == "conv3d_vae":
@@ -305,7 +281,8 @@ def main():
     # The committed counter summary covers the north-star fp16 kernel only.
     north_star = args.workload == "ns" and args.dtype == "fp16"
     prof = (read_profile_figures() if north_star else
-            {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None})
+            {"traffic": None, "mfma_busy_pct": None, "lds_bank_conflict_pct": None,
+             "counters_workload": None})
     metric = METRIC if args.workload == "ns" else (
         f"attn fwd TFLOP/s + % fp16 MFMA peak, config {args.workload} "
         f"(B{w['B']} H{w['H']} Sq{w['Sq']} Skv{w['Skv']} D{w['D']}), 1×MI355X")
@@ -343,6 +320,7 @@ def main():
         },
         "counters": {"mfma_busy_pct": prof["mfma_busy_pct"],
                      "lds_bank_conflict_pct": prof["lds_bank_conflict_pct"],
+                     "workload": prof["counters_workload"],
                      "source": os.path.relpath(TRAFFIC_FILE, ROOT)
                      if north_star and os.path.isfile(TRAFFIC_FILE) else None},
     }

@@ -3,9 +3,12 @@
 :func:`extension` returns the torch binding module (``attn(q, k, v, scale)``)
 and raises if it has not been built, so nothing silently falls back to
 another implementation. :func:`load_attention` keeps the reference loader's
-caller contract (deploy/gfx906_attn.py:62-88): it returns the module, or
-``None`` off a gfx950 device or when the library cannot be loaded, so a hook
-layer can keep its stock attention path.
+caller contract (deploy/gfx906_attn.py:28-88): on a gfx950 device it builds
+what is missing or out of date (the kernel library with hipcc, once, with a
+failure marker that stops retries; the binding with
+``torch.utils.cpp_extension.load``) and returns the module; off gfx950, or
+when a build or load fails, it returns ``None`` so a hook layer keeps its
+stock attention path. The first outcome is cached.
 """
 
 from __future__ import annotations
@@ -95,17 +98,26 @@ def is_gfx950() -> bool:
 def load_attention():
     """Return the extension module (has ``attn(q, k, v, scale)``) or ``None``.
 
-    ``None`` off gfx950 or when the built library cannot be loaded; the first
-    outcome is cached, as in deploy/gfx906_attn.py:62-88. Building is not
-    attempted here: the libraries are built ahead of time, in-tree.
+    ``None`` off gfx950, when the kernel library cannot be built (see
+    gfx906_amd.build.ensure_kernel_lib: a failed build is not retried until a
+    source changes) or when the binding cannot be built or loaded. The first
+    outcome is cached, as in deploy/gfx906_attn.py:62-88.
     """
-    global _module, _attempted
+    global _module, _attempted, _ext
     if _attempted:
         return _module
     _attempted = True
     try:
         if not is_gfx950():
             return None
+        from . import build
+
+        if not build.ensure_kernel_lib():
+            return None
+        if build.extension_stale():
+            mod = build.load_extension()
+            sys.modules[EXT_NAME] = mod
+            _ext = mod
         _module = extension()
         logger.info("gfx950 attention kernel loaded")
     except Exception as exc:  # noqa: BLE001 - caller keeps its stock attention

@@ -83,8 +83,9 @@ int attn_fwd_split(const void* q, const void* k, const void* v, void* o,
                    void* workspace, size_t workspace_bytes);
 
 /* Message for the last failed launch()/attn_fwd()/attn_fwd_ex()/
- * attn_fwd_split() on the calling thread, or NULL if the last call succeeded. No counterpart in the
- * reference, whose launch() (attn_kernel.hip:710-742) never reports errors. */
+ * attn_fwd_split() on the calling thread, or NULL if the last call
+ * succeeded. No counterpart in the reference, whose launch()
+ * (attn_kernel.hip:710-742) never reports errors. */
 const char* attn_last_error(void);
 
 #ifdef __cplusplus

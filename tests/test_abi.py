@@ -224,17 +224,6 @@ def test_conv3d_rejects_without_launch(kw, msg):
     assert rc == 1 and msg in err, err
 
 
-def test_mfma_ceiling_library_rejects_bad_arguments_without_launch():
-    from gfx906_amd.build import CEILING_LIB
-
-    lib = ctypes.CDLL(str(CEILING_LIB))
-    lib.mfma_ceiling.restype = ctypes.c_int
-    tf, ghz = ctypes.c_double(), ctypes.c_double()
-    for mode, iters, reps in ((5, 10, 1), (-1, 10, 1), (0, 0, 1), (0, 10, 0)):
-        assert lib.mfma_ceiling(mode, iters, reps, ctypes.byref(tf), ctypes.byref(ghz)) == 1
-    assert lib.mfma_ceiling(0, 10, 1, None, ctypes.byref(ghz)) == 1
-
-
 def test_ex_head_dim_stride_rules():
     # outside D == 512 with token-contiguous k/v the head dim must be contiguous
     rc, err = _ex(D=64, q=(2 * 16 * 64, 16 * 64, 1, 16))

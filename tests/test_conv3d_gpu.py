@@ -44,7 +44,7 @@ def check(got, exact, what):
 
 
 def direct(x, w, b, res, stride, out=None):
-    return kitchen._conv3d_into(x, w, b, res, list(stride), out=out)
+    return kitchen.try_kernel(x, w, b, res, list(stride), out=out)
 
 
 @pytest.mark.parametrize("i", range(len(oc.REF_CASES)))
@@ -116,7 +116,7 @@ def test_x_z_window_view():
     buf, w, b, _ = oc.make_case((1, 128, 8, 34, 34), (256, 3, 3, 3), (1, 1, 1), True, False, 121)
     bd = to_dev(buf).contiguous(memory_format=CL)
     xwin = bd[:, :, 2:7]
-    assert kitchen._ndhwc_strides(xwin) is not None
+    assert kitchen.ndhwc_strides(xwin) is not None
     got = direct(xwin, to_dev(w), to_dev(b), None, (1, 1, 1))
     check(got, oc.conv3d_gemm(buf[:, :, 2:7], w, b), "x z-window view")
 
@@ -192,7 +192,7 @@ def test_capi_matches_op():
     k, _, t, r, s = w.shape
     Z, P, Q = oc.output_size(d, h, ww, t, r, s, (1, 1, 1))
     ints = [n, d, h, ww, c, k, t, r, s, 1, 1, 1, Z, P, Q]
-    xs, os_ = kitchen._packed_strides(xd.shape), kitchen._packed_strides(out.shape)
+    xs, os_ = kitchen.packed_strides(xd.shape), kitchen.packed_strides(out.shape)
     args = ([ctypes.c_void_p(p) for p in (xd.data_ptr(), wd.data_ptr(), bd.data_ptr(),
                                            rd.data_ptr(), out.data_ptr())]
             + [ctypes.c_int(v) for v in ints] + [ctypes.c_long(n * Z * P * Q)]

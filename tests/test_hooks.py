@@ -89,9 +89,21 @@ def test_eligibility_rejections():
     assert not hooks.eligible(cpu, cpu, cpu, 4, None, {})                    # not on the GPU
 
 
+def test_decline_reasons_name_the_rule():
+    q = FakeCuda((2, 4, 10, 128))
+    assert hooks.decline_reason(q, q, q, 4, None, {}) is None
+    assert hooks.decline_reason(q, q, q, 4, object(), {}) == "mask"
+    assert hooks.decline_reason(q, q, q, 4, None, {"enable_gqa": True}) == "grouped-query attention"
+    assert hooks.decline_reason(q, q, q, 2, None, {}) == "head count differs from `heads`"
+    assert hooks.decline_reason(FakeCuda((2, 4, 10, 96)), FakeCuda((2, 4, 10, 96)),
+                                FakeCuda((2, 4, 10, 96)), 4, None, {}) == "head dim 96"
+    assert hooks.decline_reason(q, FakeCuda((2, 4, 10, 64)), FakeCuda((2, 4, 10, 64)), 4, None,
+                                {}) == "q and k disagree on batch, heads or head dim"
+
+
 # -- container function ------------------------------------------------------------------------
 
-def test_container_falls_back_to_stock_when_ineligible():
+def test_container_ineligible_goes_to_stock():
     calls = []
 
     def stock(q, k, v, heads, **kw):
@@ -100,7 +112,7 @@ def test_container_falls_back_to_stock_when_ineligible():
 
     q = torch.zeros(1, 2, 3, 128, dtype=torch.float16)  # CPU tensor: ineligible
     boxes = [Box(q), Box(q), Box(q)]
-    with mock.patch.object(hooks, "_stock_attention", stock):
+    with mock.patch.object(hooks.dit, "stock", stock):
         out = hooks.container_attn(*boxes, 2, skip_reshape=True, scale=0.5)
     assert out == "stock" and all(b.taken for b in boxes)
     assert calls[0][2]["skip_reshape"] is True and calls[0][2]["scale"] == 0.5
@@ -109,7 +121,7 @@ def test_container_falls_back_to_stock_when_ineligible():
 def test_container_requires_skip_reshape():
     called = []
     q = FakeCuda((1, 2, 3, 128))
-    with mock.patch.object(hooks, "_stock_attention", lambda *a, **k: called.append(1) or "s"), \
+    with mock.patch.object(hooks.dit, "stock", lambda *a, **k: called.append(1) or "s"), \
             mock.patch.object(loader, "load_attention", side_effect=AssertionError):
         assert hooks.container_attn(Box(q), Box(q), Box(q), 2, skip_reshape=False) == "s"
     assert called
@@ -148,6 +160,26 @@ def test_container_kernel_path_layout_and_bf16():
     assert out_bhsd.shape == (2, 3, 5, 16)
 
 
+def test_container_kernel_error_falls_back_to_stock():
+    """A call the kernel raises on (e.g. a size it rejects) runs on the stock
+    path with the original arguments."""
+    stock_calls = []
+
+    def stock(q, k, v, heads, **kw):
+        stock_calls.append((q, heads, kw))
+        return "stock"
+
+    mod = types.SimpleNamespace(attn=mock.Mock(side_effect=RuntimeError("kernel: too large")))
+    q = torch.zeros(1, 2, 3, 128, dtype=torch.float16)
+    with mock.patch.object(hooks, "eligible", return_value=True), \
+            mock.patch.object(loader, "load_attention", return_value=mod), \
+            mock.patch.object(hooks.dit, "stock", stock):
+        assert hooks.container_attn(Box(q), Box(q), Box(q), 2, skip_reshape=True,
+                                    scale=0.25) == "stock"
+    mod.attn.assert_called_once()
+    assert stock_calls[0][0] is q and stock_calls[0][2]["scale"] == 0.25
+
+
 # -- VAE hook (reference test_vae_hook.py:11-68) -------------------------------------------
 
 def test_vae_factory_preserves_selected_fallback():
@@ -164,7 +196,7 @@ def test_vae_factory_preserves_selected_fallback():
         model = types.SimpleNamespace(normal_attention=normal, pytorch_attention=pytorch,
                                       vae_attention=lambda s=selected: s)
         with mock.patch.dict(sys.modules, fake_comfy(model=model)), \
-                mock.patch.object(hooks, "_stock_normal_attention", None):
+                mock.patch.object(hooks.vae, "model", None):
             hooks.install_vae_hook()
             fn = model.vae_attention()
             if selected is other:
@@ -227,10 +259,10 @@ def test_install_sets_container_function_once():
     attention = types.SimpleNamespace(optimized_attention=opt)
     with mock.patch.object(loader, "is_gfx950", return_value=True), \
             mock.patch.dict(sys.modules, fake_comfy(attention=attention)), \
-            mock.patch.object(hooks, "_stock_attention", None):
+            mock.patch.object(hooks.dit, "stock", None):
         hooks.install()
         assert opt.container_function is hooks.container_attn
-        assert hooks._stock_attention is opt
+        assert hooks.dit.stock is opt
         hooks.install()  # second call: no change
         assert opt.container_function is hooks.container_attn
 
@@ -241,6 +273,6 @@ def test_install_leaves_existing_container_function():
     attention = types.SimpleNamespace(optimized_attention=opt)
     with mock.patch.object(loader, "is_gfx950", return_value=True), \
             mock.patch.dict(sys.modules, fake_comfy(attention=attention)), \
-            mock.patch.object(hooks, "_stock_attention", None):
+            mock.patch.object(hooks.dit, "stock", None):
         hooks.install()
     assert opt.container_function is sentinel

@@ -34,7 +34,7 @@ def test_dit_container_call(dtype, D):
     q, k, v = make_inputs(2, 6, 333, 333, D, seed=D)
     qd, kd, vd = (t.to("cuda", dtype) for t in (q, k, v))
     with pytest.MonkeyPatch.context() as mp:
-        mp.setattr(hooks, "_stock_attention", None)  # the kernel path must be taken
+        mp.setattr(hooks.dit, "stock", None)  # the kernel path must be taken
         out = hooks.container_attn(Box(qd), Box(kd), Box(vd), 6, skip_reshape=True)
     torch.cuda.synchronize()
     assert out.dtype == dtype and out.shape == (2, 333, 6 * D)

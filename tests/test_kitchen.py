@@ -41,20 +41,20 @@ def cl(shape, dtype=torch.float16):
 
 def test_ndhwc_strides():
     x = cl((2, 16, 3, 5, 7))
-    assert kitchen._ndhwc_strides(x) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
-    assert kitchen._ndhwc_strides(x[:, :, 1:3]) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
-    assert kitchen._ndhwc_strides(torch.zeros(2, 16, 3, 5, 7)) is None        # NCDHW
-    assert kitchen._ndhwc_strides(cl((1, 4, 3, 5, 7))) is None                 # C=4: strides % 8
-    assert kitchen._ndhwc_strides(torch.zeros(2, 16, 3, 5)) is None            # not 5-D
-    assert kitchen._packed_strides((2, 16, 3, 5, 7)) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
+    assert kitchen.ndhwc_strides(x) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
+    assert kitchen.ndhwc_strides(x[:, :, 1:3]) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
+    assert kitchen.ndhwc_strides(torch.zeros(2, 16, 3, 5, 7)) is None        # NCDHW
+    assert kitchen.ndhwc_strides(cl((1, 4, 3, 5, 7))) is None                 # C=4: strides % 8
+    assert kitchen.ndhwc_strides(torch.zeros(2, 16, 3, 5)) is None            # not 5-D
+    assert kitchen.packed_strides((2, 16, 3, 5, 7)) == (3 * 5 * 7 * 16, 5 * 7 * 16, 7 * 16, 16)
 
 
 def test_tensors_overlap():
     buf = torch.zeros(100)
-    assert kitchen._tensors_overlap(buf[0:10], buf[5:15])
-    assert not kitchen._tensors_overlap(buf[0:10], buf[10:20])
-    assert not kitchen._tensors_overlap(buf, torch.zeros(100))
-    assert kitchen._tensors_overlap(buf[::2], buf[1::2])  # interleaved: extents intersect
+    assert kitchen.may_overlap(buf[0:10], buf[5:15])
+    assert not kitchen.may_overlap(buf[0:10], buf[10:20])
+    assert not kitchen.may_overlap(buf, torch.zeros(100))
+    assert kitchen.may_overlap(buf[::2], buf[1::2])  # interleaved: extents intersect
 
 
 # -- arguments passed to the op ----------------------------------------------------------------
@@ -63,11 +63,11 @@ def test_packed_inputs_bias_residual(fake_ext):
     x, w = cl((2, 16, 5, 6, 7)), cl((24, 16, 3, 3, 3))
     b = torch.zeros(24, dtype=torch.float16)
     res = cl((2, 24, 3, 4, 5))
-    out = kitchen._conv3d_into(x, w, b, res, [1, 1, 1])
+    out = kitchen.try_kernel(x, w, b, res, [1, 1, 1])
     (c,) = fake_ext.calls
     assert c["dims"] == [2, 5, 6, 7, 16, 24, 3, 3, 3, 1, 1, 1, 3, 4, 5]
-    assert c["xs"] == list(kitchen._packed_strides(x.shape))
-    assert c["os"] == list(kitchen._packed_strides(out.shape)) == c["rs"]
+    assert c["xs"] == list(kitchen.packed_strides(x.shape))
+    assert c["os"] == list(kitchen.packed_strides(out.shape)) == c["rs"]
     assert out.shape == (2, 24, 3, 4, 5) and out.is_contiguous(memory_format=CL)
     assert c["out"] is out and c["res"] is res
 
@@ -76,7 +76,7 @@ def test_ncdhw_input_converted_and_strided_output(fake_ext):
     x, w = torch.zeros(1, 16, 4, 9, 9, dtype=torch.float16), cl((8, 16, 1, 3, 3))
     big = cl((1, 8, 10, 4, 4))
     out = big[:, :, 2:6]
-    got = kitchen._conv3d_into(x, w, None, None, (1, 2, 2), out=out)
+    got = kitchen.try_kernel(x, w, None, None, (1, 2, 2), out=out)
     (c,) = fake_ext.calls
     assert got is out and c["x"].is_contiguous(memory_format=CL)
     assert c["dims"][12:] == [4, 4, 4]
@@ -86,7 +86,7 @@ def test_ncdhw_input_converted_and_strided_output(fake_ext):
 def test_residual_may_be_out(fake_ext):
     x, w = cl((1, 8, 3, 6, 6)), cl((8, 8, 1, 3, 3))
     out = cl((1, 8, 3, 4, 4))
-    assert kitchen._conv3d_into(x, w, None, out, (1, 1, 1), out=out) is out
+    assert kitchen.try_kernel(x, w, None, out, (1, 1, 1), out=out) is out
     assert fake_ext.calls[0]["res"] is out
 
 
@@ -116,13 +116,27 @@ def test_declines(fake_ext, case):
         out = big[:, :24, :3, :4, :5]
     elif case == "out_batch0":
         out = cl((1, 24, 3, 4, 5)).expand(2, 24, 3, 4, 5)
-    assert kitchen._conv3d_into(x, w, b, res, stride, out=out) is None
+    assert kitchen.try_kernel(x, w, b, res, stride, out=out) is None
+    assert not fake_ext.calls
+
+
+def test_plan_names_decline_reasons(fake_ext):
+    x, w = cl((2, 16, 5, 6, 7)), cl((24, 16, 3, 3, 3))
+    assert isinstance(kitchen.plan(x, w, None, None, (1, 1, 1)), kitchen.ConvCall)
+    assert kitchen.plan(x, cl((20, 16, 3, 3, 3)), None, None, (1, 1, 1)) == \
+        "C and K must be positive multiples of 8"
+    assert kitchen.plan(x, w, None, None, (1, 0, 1)) == "stride below 1"
+    assert kitchen.plan(cl((2, 16, 2, 6, 7)), w, None, None, (1, 1, 1)) == \
+        "input smaller than the filter"
+    big = cl((2, 24, 5, 6, 7))
+    assert kitchen.plan(big[:, :16], w, None, None, (1, 1, 1), out=big[:, :24, :3, :4, :5]) == \
+        "out shares memory with an input"
     assert not fake_ext.calls
 
 
 def test_bad_out_raises(fake_ext):
     with pytest.raises(ValueError):
-        kitchen._conv3d_into(cl((1, 8, 3, 6, 6)), cl((8, 8, 1, 3, 3)), None, None, (1, 1, 1),
+        kitchen.try_kernel(cl((1, 8, 3, 6, 6)), cl((8, 8, 1, 3, 3)), None, None, (1, 1, 1),
                              out=cl((1, 8, 3, 4, 5)))
 
 

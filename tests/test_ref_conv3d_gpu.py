@@ -43,7 +43,7 @@ def run_ref(lib, x, w, bias, res, stride):
     Z, P, Q = oc.output_size(d, h, ww, t, r, s, stride)
     out = torch.empty((n, k, Z, P, Q), dtype=torch.float16, device=x.device,
                       memory_format=CL)
-    xs, os_ = kitchen._packed_strides(x.shape), kitchen._packed_strides(out.shape)
+    xs, os_ = kitchen.packed_strides(x.shape), kitchen.packed_strides(out.shape)
     rs = os_ if res is not None else (0, 0, 0, 0)
     ptr = [ctypes.c_void_p(0 if t_ is None else t_.data_ptr()) for t_ in (x, w, bias, res, out)]
     lib.launch_conv3d(*ptr, *[ctypes.c_int(v) for v in (n, d, h, ww, c, k, t, r, s, *stride,
@@ -66,7 +66,7 @@ def dev_case(i):
 def test_reference_conv3d_agrees_with_oracle_and_ours(ref, i):
     (x, w, b, res, stride), (xd, wd, bd, rd, _) = dev_case(i)
     o_ref = run_ref(ref, xd, wd, bd, rd, stride)
-    o_new = kitchen._conv3d_into(xd, wd, bd, rd, list(stride))
+    o_new = kitchen.try_kernel(xd, wd, bd, rd, list(stride))
     torch.cuda.synchronize()
     exact = torch.from_numpy(oc.conv3d_gemm(x, w, b, res, stride))
     r, nw = o_ref.double().cpu(), o_new.double().cpu()
@@ -97,9 +97,9 @@ def test_vae_layer_timing(ref):
     b = torch.from_numpy(g.standard_normal(512).astype(np.float16)).cuda()
     xd, wd = x.cuda().contiguous(memory_format=CL), w.cuda().contiguous(memory_format=CL)
     flop = 2 * 1 * 6 * 62 * 62 * 512 * 512 * 27
-    t_new = _time(lambda: kitchen._conv3d_into(xd, wd, b, None, [1, 1, 1]))
+    t_new = _time(lambda: kitchen.try_kernel(xd, wd, b, None, [1, 1, 1]))
     t_ref = _time(lambda: run_ref(ref, xd, wd, b, None, (1, 1, 1)))
-    o_new = kitchen._conv3d_into(xd, wd, b, None, [1, 1, 1])
+    o_new = kitchen.try_kernel(xd, wd, b, None, [1, 1, 1])
     o_ref = run_ref(ref, xd, wd, b, None, (1, 1, 1))
     torch.cuda.synchronize()
     print(f"VAE layer 512->512 3x3x3 on 1x8x64x64: gfx950 {t_new:.3f} ms "
