@@ -53,6 +53,7 @@
 #include <math.h>
 #include <type_traits>
 #include <algorithm>
+#include <mutex>
 
 #include "gfx906_amd_attn.h"
 
@@ -1411,12 +1412,66 @@ extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr
 
 namespace {
 
-// attn_fwd_ex (workspace_bytes == SIZE_MAX: never split) and attn_fwd_split.
+// Workspace of attn_fwd_split_static: the split-key partial results live in
+// this file-scope device array instead of caller memory. Each GPU the
+// library runs on holds its own copy (from the first use until the process
+// ends). Host code must not pass `scratch` itself to a kernel (on the host it
+// names a stand-in, not device memory): it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device. The kernels write
+// every workspace entry the merge reads within the same call, so nothing is
+// cleared between calls; calls that overlap on one GPU share the array and
+// race.
+constexpr size_t kScratchBytes = size_t(96) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's address of `scratch`, for the device `stream` belongs to (the
+// current device for the null stream). Returns 0, or an attn_fwd status with
+// the error message set.
+int device_scratch(hipStream_t stream, void** out) {
+    int dev = 0, cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) {
+        dev = cur;
+        if (stream) e = hipStreamGetDevice(stream, &dev);
+    }
+    if (e != hipSuccess) {
+        set_err(hipGetErrorString(e));
+        return 2;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail("attn: device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+            set_err(hipGetErrorString(e));
+            return 2;
+        }
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) {
+            const hipError_t r = hipSetDevice(cur);
+            if (e == hipSuccess) e = r;
+        }
+        if (e != hipSuccess || !p) {
+            set_err(e != hipSuccess ? hipGetErrorString(e) : "attn: no device address for scratch");
+            return 2;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+// attn_fwd_ex (workspace_bytes == SIZE_MAX: never split), attn_fwd_split
+// and, with use_scratch, attn_fwd_split_static (workspace: the static scratch).
 int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
                   int Skv, int D, float scale, hipStream_t stream, int dtype,
                   const long long* q_strides, const long long* k_strides,
                   const long long* v_strides, const long long* o_strides, void* workspace,
-                  size_t workspace_bytes) {
+                  size_t workspace_bytes, bool use_scratch = false) {
     g_err[0] = 0;
     auto pick = [](const long long* p, Strides dflt) {
         return p ? Strides{p[0], p[1], p[2], p[3]} : dflt;
@@ -1455,6 +1510,16 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     if (workspace_bytes != (size_t)-1) {  // attn_fwd_split: split the keys if it pays
         const SplitPlan p = plan_split(B, H, Sq, Skv, D);
         const size_t need = split_ws_bytes(p, B, H, Sq, D);
+        if (need && use_scratch) {
+            if (need > kScratchBytes) {
+                set_err("attn: this problem's split workspace exceeds the static scratch "
+                        "(attn_split_scratch_capacity()); use attn_fwd_split with a workspace");
+                return 1;
+            }
+            const int rc = device_scratch(stream, &workspace);
+            if (rc) return rc;
+            workspace_bytes = kScratchBytes;
+        }
         if (need) {
             if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16) {
                 set_err("attn: workspace missing, misaligned or smaller than "
@@ -1502,6 +1567,17 @@ extern "C" int attn_fwd_split(const void* q, const void* k, const void* v, void*
     if (workspace_bytes == (size_t)-1) workspace_bytes -= 1;
     return attn_fwd_impl(q, k, v, o, B, H, Sq, Skv, D, scale, stream, dtype, q_strides, k_strides,
                          v_strides, o_strides, workspace, workspace_bytes);
+}
+
+extern "C" size_t attn_split_scratch_capacity(void) { return kScratchBytes; }
+
+extern "C" int attn_fwd_split_static(const void* q, const void* k, const void* v, void* o, int B,
+                                     int H, int Sq, int Skv, int D, float scale,
+                                     hipStream_t stream, int dtype, const long long* q_strides,
+                                     const long long* k_strides, const long long* v_strides,
+                                     const long long* o_strides) {
+    return attn_fwd_impl(q, k, v, o, B, H, Sq, Skv, D, scale, stream, dtype, q_strides, k_strides,
+                         v_strides, o_strides, nullptr, 0, true);
 }
 
 extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,

@@ -74,6 +74,10 @@ def capi() -> ctypes.CDLL:
     lib.attn_fwd_split.restype = ctypes.c_int
     lib.attn_split_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.attn_split_workspace_bytes.restype = ctypes.c_size_t
+    lib.attn_fwd_split_static.argtypes = lib.attn_fwd_ex.argtypes
+    lib.attn_fwd_split_static.restype = ctypes.c_int
+    lib.attn_split_scratch_capacity.argtypes = []
+    lib.attn_split_scratch_capacity.restype = ctypes.c_size_t
     lib.attn_last_error.argtypes = []
     lib.attn_last_error.restype = ctypes.c_char_p
     return lib

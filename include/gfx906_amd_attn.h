@@ -82,9 +82,28 @@ int attn_fwd_split(const void* q, const void* k, const void* v, void* o,
                    const long long* v_strides, const long long* o_strides,
                    void* workspace, size_t workspace_bytes);
 
+/* attn_fwd_split() that allocates nothing: the split partial results go to a
+ * static device array of the library, attn_split_scratch_capacity() bytes
+ * (96 MiB) on each GPU it runs on, held until the process ends. For callers
+ * that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. Problems whose split
+ * workspace (attn_split_workspace_bytes()) exceeds the capacity are rejected
+ * with status 1 before anything runs; problems that do not split use no
+ * scratch. Calls that overlap on one GPU share the array and must not run
+ * concurrently. Same arguments, results and return codes as attn_fwd_split()
+ * otherwise. No counterpart in the reference. */
+int attn_fwd_split_static(const void* q, const void* k, const void* v, void* o,
+                          int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream,
+                          int dtype, const long long* q_strides, const long long* k_strides,
+                          const long long* v_strides, const long long* o_strides);
+
+/* Bytes of the static scratch attn_fwd_split_static() uses. No counterpart in
+ * the reference. */
+size_t attn_split_scratch_capacity(void);
+
 /* Message for the last failed launch()/attn_fwd()/attn_fwd_ex()/
- * attn_fwd_split() on the calling thread, or NULL if the last call
- * succeeded. No counterpart in the reference, whose launch()
+ * attn_fwd_split()/attn_fwd_split_static() on the calling thread, or NULL if
+ * the last call succeeded. No counterpart in the reference, whose launch()
  * (attn_kernel.hip:710-742) never reports errors. */
 const char* attn_last_error(void);
 

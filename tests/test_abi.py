@@ -259,6 +259,23 @@ def test_split_workspace_bytes():
         assert lib.attn_split_workspace_bytes(*bad) == 0
 
 
+def test_split_static_scratch_capacity_and_rejection():
+    lib = gfx906_amd.capi()
+    cap = lib.attn_split_scratch_capacity()
+    assert cap == 96 << 20
+    # One D=512 head of 25600 queries splits in two: 2*25600*(512+2)*4 bytes > 96 MiB.
+    need = lib.attn_split_workspace_bytes(1, 1, 25600, 4096, 512)
+    assert need > cap
+    rc = lib.attn_fwd_split_static(P, P, P, P, 1, 1, 25600, 4096, 512, 0.1, None, 0,
+                                   None, None, None, None)
+    assert rc == 1 and b"exceeds the static scratch" in lib.attn_last_error()
+    # Within capacity, arguments are validated as for attn_fwd_split.
+    assert lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 512) <= cap
+    rc = lib.attn_fwd_split_static(None, None, None, None, 1, 1, 4096, 4096, 512, 0.1, None, 0,
+                                   None, None, None, None)
+    assert rc == 1 and b"null" in lib.attn_last_error()
+
+
 def test_split_rejects_missing_or_short_workspace():
     lib = gfx906_amd.capi()
     need = lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 512)
