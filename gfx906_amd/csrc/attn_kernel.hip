@@ -54,6 +54,7 @@
 #include <type_traits>
 #include <algorithm>
 #include <mutex>
+#include <stdlib.h>
 
 #include "gfx906_amd_attn.h"
 
@@ -453,13 +454,14 @@ attn_fwd_pipe(const KArgs a) {
     }
 
     f32x4 oacc[NOB][2];
-    // Row sums on the matrix pipe (D = 128): lacc[nb] += A1 * P with A1 = 1
-    // in row 0 and 0 elsewhere, so accumulator row 0 (lane l%16 of lane
-    // group 0) holds the running sum of the rounded p of query 16nb + l%16.
-    // This replaces eight v_dot2 per block, which the matrix pipe cannot
-    // overlap, by two 16x16x32 MFMAs (+1.5 % north star; for D = 64, where
-    // they are 12 % more MFMA work instead of 6 %, it loses 2-3 %).
-    constexpr bool kMfmaSum = DP == 128;
+    // Row sums on the matrix pipe: lacc[nb] += A1 * P with A1 = 1 in row 0
+    // and 0 elsewhere, so accumulator row 0 (lane l%16 of lane group 0)
+    // holds the running sum of the rounded p of query 16nb + l%16. Two
+    // 16x16x32 MFMAs per block replace eight v_dot2, which the matrix pipe
+    // cannot overlap (measured: +1.5 % north star; D = 64, where they add 12 %
+    // of the block's matrix work, +6 % c5 and +1 % c3 with the exact running
+    // max below, whose rescales add VALU work).
+    constexpr bool kLazy = DP == 128;
     // Running max of each query column block. D = 128 keeps a lazy one, in
     // log2 units (s*c), raised only when some p exceeds 2^15 (rare after the
     // first blocks: every p stays finite in fp16); it starts at -1e30
@@ -470,13 +472,12 @@ attn_fwd_pipe(const KArgs a) {
     // error of up to 2^-11 relative, which on sharp rows with |o| near 4 and
     // above (c3: q, k ~ 2 N(0,1), 512 keys) moves the output past the 2e-3
     // bar.
-    float m_run[2], l_run[2];
+    float m_run[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] = f32x4{};
-        m_run[nb] = kMfmaSum ? -1e30f : -INFINITY;
-        l_run[nb] = 0.f;
+        m_run[nb] = kLazy ? -1e30f : -INFINITY;
     }
     f32x4 lacc[2] = {f32x4{}, f32x4{}};
     x8 aone;
@@ -571,13 +572,10 @@ attn_fwd_pipe(const KArgs a) {
         // (m_run's units).
         auto rescale = [&](int nb, float m_new) __attribute__((always_inline)) {
             const float alpha =
-                __builtin_amdgcn_exp2f(kMfmaSum ? m_run[nb] - m_new : (m_run[nb] - m_new) * c);
+                __builtin_amdgcn_exp2f(kLazy ? m_run[nb] - m_new : (m_run[nb] - m_new) * c);
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-            if constexpr (kMfmaSum)
-                lacc[nb] *= alpha;
-            else
-                l_run[nb] *= alpha;
+            lacc[nb] *= alpha;
             m_run[nb] = m_new;
         };
         auto lane_max = [&](const f32x4 (&S)[2][2], int nb) __attribute__((always_inline)) {
@@ -600,8 +598,8 @@ attn_fwd_pipe(const KArgs a) {
         //  gives p = exp2(fma(s, c, -RN(s*c))), within 2^-20 of 1, which
         //  rounds to exactly 1.0.
         auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
-            if constexpr (kMfmaSum) {
-                float lp[2];  // unused: the row sums come from the MFMAs below
+            float lp[2];  // unused: the row sums come from the MFMAs below
+            if constexpr (kLazy) {
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
                     block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
@@ -612,11 +610,6 @@ attn_fwd_pipe(const KArgs a) {
                         block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb], c, lp[nb]);
                     }
                 }
-                // Row sums of this block's P: issued here, where the wave's
-                // stream is mostly VALU work (+0.6 % north star against
-                // issuing them with the PV MFMAs), after any rescale of lacc.
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
             } else {
                 const float lm0 = lane_max(S, 0), lm1 = lane_max(S, 1);
                 if (__any(lm0 > m_run[0] || lm1 > m_run[1])) {
@@ -627,8 +620,13 @@ attn_fwd_pipe(const KArgs a) {
                 }
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
-                    block_exp<T, true>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, l_run[nb]);
+                    block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, lp[nb]);
             }
+            // Row sums of this block's P: issued here, where the wave's
+            // stream is mostly VALU work (+0.6 % north star against issuing
+            // them with the PV MFMAs), after any rescale of lacc.
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
         };
 
         f32x4 Sa[2][2], Sb[2][2];
@@ -718,7 +716,7 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int row = qrow0 + 16 * nb;
-            const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
+            const float l = quad_group_sum(lacc[nb][0]);
             if (row < Sq) {
                 const long long r = ((long long)split * a.BH + bh) * Sq + row;
                 float* wo = a.ws_o + r * D;
@@ -727,7 +725,7 @@ attn_fwd_pipe(const KArgs a) {
                     const int d0 = 16 * ob + 4 * g;
                     if (!PAD || d0 < D) *reinterpret_cast<f32x4*>(wo + d0) = oacc[ob][nb];
                 }
-                const float m = kMfmaSum ? m_run[nb] : m_run[nb] * c;  // log2 units
+                const float m = kLazy ? m_run[nb] : m_run[nb] * c;  // log2 units
                 if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m, l};
             }
         }
@@ -746,7 +744,7 @@ attn_fwd_pipe(const KArgs a) {
         char* const stg = sa + (wave & 1) * 32 * RS;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
+            const float l = quad_group_sum(lacc[nb][0]);
             const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) {
@@ -771,7 +769,7 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         const int row = qrow0 + 16 * nb;
-        const float l = quad_group_sum(kMfmaSum ? lacc[nb][0] : l_run[nb]);
+        const float l = quad_group_sum(lacc[nb][0]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         if (row < Sq) {
             T* op = Oh + row * a.so.s;
@@ -787,6 +785,232 @@ attn_fwd_pipe(const KArgs a) {
             }
         }
     }
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// D <= 64 with a short key range: K and V resident in LDS, persistent
+// workgroups.
+//
+// When a head's whole K and V fit in LDS (up to 10 tiles of 64 keys, 160 KB,
+// i.e. Skv <= 640), one workgroup of 16 waves per CU loads them once and runs
+// the query tiles assigned to it back to back (512 rows per tile, 32 per
+// wave, the same per-wave block pipeline and softmax as attn_fwd_pipe, so
+// the results are bit-identical). The main loop issues no loads into LDS and
+// no barriers: the waves drift apart, and one wave's Q loads and O stores
+// overlap the other waves' matrix work. A barrier is needed only when the
+// workgroup moves on to another head's K/V. Workgroup g of G takes query
+// tiles [g*n/G, (g+1)*n/G) of the n = B*H*ceil(Sq/512) tiles, head-major.
+struct CfgRes {
+    static constexpr int DP = 64, NW = 16, BN = 64, BM = NW * 32, NT = NW * 64;
+    static constexpr int NU = DP / 8, RB = DP * 2, TILE = BN * RB, STAGE = 2 * TILE;
+    static constexpr int MAX_TILES = 10;  // 10 x 16 KB = 160 KB, all of a CU's LDS
+};
+
+template <bool PAD, class T>
+__global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using C = CfgRes;
+    using Ring = Cfg<64, 8, 2>;  // tile geometry and load offsets shared with the ring kernel
+    using E = Elem<T>;
+    using x8 = typename E::x8;
+    constexpr int DP = C::DP, NU = C::NU, RB = C::RB, TILE = C::TILE, STAGE = C::STAGE;
+    constexpr int NQF = DP / 32, NOB = DP / 16;
+    static_assert(Ring::TILE == TILE && Ring::BLKS / Ring::NW == 1, "one 1 KB block per wave");
+    __shared__ __attribute__((aligned(1024))) char kv[C::MAX_TILES * STAGE];
+
+    const int Sq = a.Sq, D = a.D, Skv = a.Skv;
+    const float c = a.c;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const int nqt = (Sq + C::BM - 1) / C::BM;
+    const int ntiles = (Skv + C::BN - 1) / C::BN;
+    const long long items = (long long)a.BH * nqt;
+    const int first = (int)(items * blockIdx.x / gridDim.x);
+    const int last = (int)(items * (blockIdx.x + 1) / gridDim.x);
+    const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
+
+    // Loads of a head's K/V: waves 0-7 fill 1 KB block (wave % 8) of every K
+    // tile, waves 8-15 the same block of every V tile; rows past Skv load
+    // zeros.
+    int koff[1], voff[1];
+    tile_offsets<Ring, PAD>(koff, voff, D, (int)a.sk.s, (int)a.sv.s, wave & 7, lane);
+    // K (and Q) read: row 16kb + l%16 of a 32-key block, dims 32s + 8(l/16)..
+    int kaddr[NQF];
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) kaddr[s] = i * RB + ((4 * s + g) ^ kswz<NU>(i)) * 16;
+    // V^T read (two ds_read_b64_tr_b16), as in attn_fwd_pipe.
+    int vaddr[NOB];
+    {
+        const int vrow = 4 * g + (i >> 2);
+        const int vx = vswz<NU>(vrow) >> 1;
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) vaddr[ob] = vrow * RB + (ob ^ vx) * 32 + (i & 3) * 8;
+    }
+
+    f32x4 oacc[NOB][2], lacc[2];  // O^T and the row sums (MFMA, row 0), as attn_fwd_pipe
+    float m_run[2];               // exact running max in score units, as attn_fwd_pipe for D <= 64
+    x8 qf[2][NQF];
+    x8 aone;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) aone[e] = (T)(i == 0 ? 1.0f : 0.0f);
+
+    auto qk = [&](const char* st, int blk, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) S[kb][nb] = f32x4{};
+#pragma unroll
+        for (int s = 0; s < NQF; ++s)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const x8 kf = lds_read16<T>(st, kaddr[s] + (32 * blk + 16 * kb) * RB);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) S[kb][nb] = E::mma16(kf, qf[nb][s], S[kb][nb]);
+            }
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 3, 0);
+#pragma unroll
+        for (int n = 0; n < 2 * NQF - 3; ++n) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
+    };
+    auto pv = [&](const char* st, int blk, const x8 (&P)[2]) __attribute__((always_inline)) {
+        const char* sv = st + TILE;
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) {
+            const int off = vaddr[ob] + 32 * blk * RB;
+            const x8 vf = lds_read_tr2<T>(sv, off, off + 16 * RB);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 6, 0);
+#pragma unroll
+        for (int n = 0; n < NOB - 3; ++n) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
+    };
+    auto mask = [&](f32x4 (&S)[2][2], int key0) __attribute__((always_inline)) {
+        if (key0 + 32 > Skv) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
+        }
+    };
+    auto lane_max = [&](const f32x4 (&S)[2][2], int nb) __attribute__((always_inline)) {
+        const float mx = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
+        const float my = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
+        return max2(max3(mx, S[1][nb][2], S[1][nb][3]), my);
+    };
+    auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
+        const float lm0 = lane_max(S, 0), lm1 = lane_max(S, 1);
+        if (__any(lm0 > m_run[0] || lm1 > m_run[1])) {
+            const float lm[2] = {lm0, lm1};
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const float m_new = max2(m_run[nb], quad_group_max(lm[nb]));
+                const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
+                lacc[nb] *= alpha;
+                m_run[nb] = m_new;
+            }
+        }
+        float lp[2];  // unused: the row sums come from the MFMAs below
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, lp[nb]);
+            lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
+        }
+    };
+
+    int cur_bh = -1;
+    for (int item = first; item < last; ++item) {
+        const int bh = item / nqt, qt = item - bh * nqt;
+        const int b = bh / a.H, h = bh - b * a.H;
+        if (bh != cur_bh) {  // (re)load this head's K/V; wave-uniform, the same in every wave
+            if (cur_bh >= 0) lds_barrier();  // every wave is done with the previous head
+            cur_bh = bh;
+            const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+            const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+            for (int t = 0; t < ntiles; ++t) {
+                if (wave < 8)
+                    issue_tile<Ring>(Kh, t * C::BN, Skv, D, a.sk.s, kv + t * STAGE, wave, koff);
+                else
+                    issue_tile<Ring>(Vh, t * C::BN, Skv, D, a.sv.s, kv + t * STAGE + TILE,
+                                     wave - 8, voff);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads landed
+            lds_barrier();                      // ... and every wave's
+        }
+        const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+        T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
+        const int qrow0 = qt * C::BM + wave * 32 + i;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+            for (int s = 0; s < NQF; ++s) {
+                const int d0 = 32 * s + 8 * g, row = qrow0 + 16 * nb;
+                qf[nb][s] = q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
+            }
+#pragma unroll
+            for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] = f32x4{};
+            lacc[nb] = f32x4{};
+            m_run[nb] = -INFINITY;
+        }
+
+        // Block pipeline over the resident tiles, as attn_fwd_pipe's tile():
+        // the iteration for block j issues the PV MFMAs of block j-1 and the
+        // QK^T MFMAs of block j+1 around the softmax of block j. The QK^T of
+        // the block after the last one reads tile 0 and is discarded.
+        f32x4 Sa[2][2], Sb[2][2];
+        x8 Pa[2], Pb[2];
+        if (ntiles > 0) {  // (no keys: the row sums stay 0 and the rows are written as zeros)
+        qk(kv, 0, Sa);
+        for (int t = 0; t < ntiles; ++t) {
+            const char* cur = kv + t * STAGE;
+            const char* nxt = t + 1 < ntiles ? cur + STAGE : kv;
+            mask(Sa, t * C::BN);
+            if (t > 0) pv(cur - STAGE, 1, Pb);  // block 2t-1
+            qk(cur, 1, Sb);                     // block 2t+1
+            softmax(Sa, Pa);                    // block 2t
+            mask(Sb, t * C::BN + 32);
+            pv(cur, 0, Pa);                     // block 2t
+            qk(nxt, 0, Sa);                     // block 2t+2
+            softmax(Sb, Pb);                    // block 2t+1
+        }
+        pv(kv + (ntiles - 1) * STAGE, 1, Pb);  // block 2 ntiles - 1
+        }
+
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int row = qrow0 + 16 * nb;
+            const float l = quad_group_sum(lacc[nb][0]);
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+            if (row < Sq) {
+                T* op = Oh + row * a.so.s;
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob) {
+                    const int d0 = 16 * ob + 4 * g;
+                    if (!PAD || d0 < D) {
+                        const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
+                        const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
+                        *reinterpret_cast<typename E::x4*>(op + d0) =
+                            typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+                    }
+                }
+            }
+        }
+    }
+    // Loads past the end were never issued; nothing is in flight here.
 #endif
 }
 
@@ -1225,6 +1449,38 @@ void set_err(const char* msg) {
 using Cfg128 = Cfg<128, 8, 1>;  // 128 KB of LDS: one workgroup, two waves per SIMD
 using Cfg64 = Cfg<64, 8, 2>;    // 64 KB: two workgroups, four waves per SIMD
 
+int cu_count();
+
+// Query tiles of the K/V-resident kernel.
+long long kvres_items(const KArgs& a) {
+    return (long long)a.BH * ((a.Sq + CfgRes::BM - 1) / CfgRes::BM);
+}
+
+// Workgroups for attn_fwd_kvres on an unsplit D <= 64 problem, or 0 when the
+// ring kernel serves it. The resident kernel needs the head's K/V to fit in
+// LDS (1 <= Skv <= 640) and, by default, at least as many 512-row query tiles
+// as CUs (fewer leave CUs idle; the ring kernel, split if need be, spreads
+// such problems wider); it then runs one workgroup per CU. The environment
+// variable GFX906_AMD_ATTN_KVRES overrides the choice for tests: 0 = ring
+// kernel, 1 = resident kernel whatever the tile count, n > 1 = resident
+// kernel on at most n workgroups (several tiles, and heads, per workgroup).
+long long kvres_grid(const KArgs& a) {
+    if (a.D > 64 || a.Skv < 1 || a.Skv > CfgRes::MAX_TILES * CfgRes::BN) return 0;
+    const long long items = kvres_items(a), cus = cu_count();
+    const char* env = getenv("GFX906_AMD_ATTN_KVRES");
+    const long long force = env ? atoll(env) : -1;
+    if (force == 0) return 0;
+    if (force == 1) return std::min(items, cus);
+    if (force > 1) return std::min(items, force);
+    // The ring kernel runs whole groups of four 64-key tiles: with a multiple
+    // of four tiles it is the faster of the two (c3, 8 tiles: 0.076 against
+    // 0.082 ms on MI355X); otherwise its padding tiles cost more than the
+    // resident kernel saves (2 x 16 x 4096 queries, 77 keys: 0.018 against
+    // 0.014 ms; 640 keys: 0.109 against 0.100 ms).
+    const int ntiles = (a.Skv + CfgRes::BN - 1) / CfgRes::BN;
+    return items >= cus && ntiles % 4 ? cus : 0;
+}
+
 template <class T, bool SPLIT>
 void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
     const int D = a.D;
@@ -1238,6 +1494,16 @@ void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
         dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * nwg);
         hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T, SPLIT>), grid, dim3(Cfg128::NT), 0, s, a);
     } else {
+        if constexpr (!SPLIT) {
+            if (const long long wgs = kvres_grid(a)) {
+                const dim3 grid((unsigned)wgs);
+                if (D == 64)
+                    hipLaunchKernelGGL((attn_fwd_kvres<false, T>), grid, dim3(CfgRes::NT), 0, s, a);
+                else
+                    hipLaunchKernelGGL((attn_fwd_kvres<true, T>), grid, dim3(CfgRes::NT), 0, s, a);
+                return;
+            }
+        }
         dim3 grid((unsigned)((a.Sq + Cfg64::BM - 1) / Cfg64::BM) * nwg);
         if (D == 64)
             hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T, SPLIT>), grid, dim3(Cfg64::NT), 0, s, a);
