@@ -48,6 +48,12 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics",
+    # MFMAs the compiler emits keep their accumulators in VGPRs. Only
+    # attn_fwd_d512w (one wave per SIMD, 512 registers) is affected: its
+    # score MFMAs then accumulate in VGPRs beside Q, while its O^T
+    # accumulator is pinned to AGPRs by inline asm. Every other kernel has at
+    # most 256 registers per lane and is compiled identically either way.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 KERNEL_SOURCES = [CSRC / "attn_kernel.hip", CSRC / "conv3d_kernel.hip"]

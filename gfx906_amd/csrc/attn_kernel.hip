@@ -42,9 +42,12 @@
 //    on almost every block); D <= 64 keeps the exact running max (limit 1:
 //    a row's dominant weight is exactly 1.0); D = 512 uses limit 2^8.
 //  * The row sum l is accumulated from the rounded P, so numerator and
-//    denominator see the same rounded weights: for D = 128 on the matrix pipe
-//    (one more 16x16x32 MFMA per column block, A = a 0/1 row selector), for
-//    D <= 64 with v_dot2_f32_{f16,bf16} against 1.0.
+//    denominator see the same rounded weights: for D <= 128 on the matrix
+//    pipe (one more 16x16x32 MFMA per column block, A = a 0/1 row selector),
+//    for D = 512 with v_dot2_f32_{f16,bf16} against 1.0.
+//  * D = 512 runs 32 query rows per wave at one wave per SIMD, its O^T
+//    accumulator in AGPRs (attn_fwd_d512w), so that each K or V fragment read
+//    from LDS feeds two MFMAs.
 //  * Output rows are normalised by 1/l and rounded to the input type (RNE),
 //    as the reference does for fp16 (attn_kernel.hip:497-511). Rows of a head
 //    with Skv == 0 are written as zeros (the reference leaves them unwritten).
@@ -156,6 +159,37 @@ struct Elem<bf16> {
         return __builtin_amdgcn_fdot2_f32_bf16(h, x2{(bf16)1.0f, (bf16)1.0f}, acc, false);
     }
 };
+
+// O^T accumulation of attn_fwd_d512w with the accumulator pinned to AGPRs:
+// its 256 accumulator registers fill the AGPR file, and the 128 registers of
+// Q and the score accumulators must stay in VGPRs, a split the compiler's
+// own register assignment does not find. The instruction is therefore
+// written out, and the wait states the compiler inserts around MFMAs it
+// knows of are provided by agpr_fence / vgpr_fence around its operands:
+//  * a VALU write of srcB (P) or of the accumulator (initialisation,
+//    rescale) needs 2 wait states before the MFMA reads it;
+//  * a VALU read of the accumulator needs the MFMA to have completed: the
+//    fence before the epilogue (and the rare rescale) gives 24.
+// Every such producer-consumer pair passes through a fence by data
+// dependence, so the fences hold whatever order the scheduler picks; the
+// MFMA's srcA (V from LDS) is ordered by the compiler's lgkmcnt waits, which
+// cover inline-asm operands.
+template <class T>
+__device__ __forceinline__ void mma16_agpr(f32x4& acc, typename Elem<T>::x8 a,
+                                           typename Elem<T>::x8 b) {
+    if constexpr (std::is_same<T, f16>::value)
+        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    else
+        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// 2 wait states after a VALU write, before an MFMA reads the registers.
+__device__ __forceinline__ void agpr_fence2(f32x4& x) { asm("s_nop 1" : "+a"(x)); }
+template <class X8>
+__device__ __forceinline__ void vgpr_fence2(X8& x, X8& y) { asm("s_nop 1" : "+v"(x), "+v"(y)); }
+// 24 wait states after an MFMA wrote the registers, before a VALU reads them.
+__device__ __forceinline__ void agpr_fence24(f32x4& a, f32x4& b, f32x4& c, f32x4& d) {
+    asm("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(a), "+a"(b), "+a"(c), "+a"(d));
+}
 
 // 16-byte global load of 8 elements.
 template <class T>
@@ -1389,6 +1423,291 @@ attn_fwd_d512(const KArgs a) {
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// D = 512, wide waves: 32 query rows per wave, one wave per SIMD.
+//
+// In attn_fwd_d512 (16 rows per wave) every K or V fragment read from LDS
+// feeds one MFMA: 1 KB of LDS per 16x16x32 MFMA, more than the LDS delivers
+// at the matrix pipe's rate (16-byte reads about 190 bytes per clock per CU,
+// the transposed V reads about 120, against 256 needed). Here each fragment
+// feeds two MFMAs (one per 16-row column block), halving LDS bytes per FLOP.
+// The O^T accumulator (32 rows x 512 dims, fp32) is 256 registers and Q is
+// 128, so the wave runs alone on its SIMD (512 registers, the accumulator in
+// AGPRs); the D = 512 work per tile (128 MFMAs against 16 exponentials per
+// lane) leaves the VALU little to hide behind a second wave.
+//
+// K and V tiles of 32 keys have two LDS buffers each. The iteration for tile
+// t runs the QK^T MFMAs of tile t+1 (K buffer (t+1)&1) in the same basic
+// block as the softmax of tile t (scores from the previous iteration), then
+// the PV MFMAs of tile t (V buffer t&1); K(t+2) and V(t+1) load meanwhile
+// into the buffers the barrier opening the iteration released. Loads past
+// the last tile have an empty buffer range and write zeros, so every
+// iteration has the same instruction stream.
+//
+// The arithmetic is attn_fwd_d512's, operation for operation: the same two
+// MFMA chains per score block, P, row sums, rescale test (per 16-row column
+// block, the rows of one attn_fwd_d512 wave) and O accumulation, so the two
+// kernels' outputs are bit-identical.
+struct Cfg512W {
+    static constexpr int DP = 512, NW = 4, BN = 32, BM = NW * 32, NT = NW * 64;
+    static constexpr int KS = Cfg512::KS, VS = Cfg512::VS;  // padded rows (bank-conflict free)
+    static constexpr int TILE = BN * KS;                   // one K or V tile
+    static constexpr int NLD = BN / NW;                    // rows per wave per tile, per tensor
+};
+static_assert(Cfg512W::BM == Cfg512::BM, "same query tiling as attn_fwd_d512 (grid, split plan)");
+
+// grid: ceil(Sq / 128) * B*H workgroups (times nsplit); block: 256 threads.
+template <class T, bool SPLIT>
+__global__ void __launch_bounds__(Cfg512W::NT, 1)
+attn_fwd_d512w(const KArgs a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using C = Cfg512W;
+    using E = Elem<T>;
+    using x8 = typename E::x8;
+    constexpr int D = C::DP, BN = C::BN, NLD = C::NLD;
+    constexpr int NQF = D / 32;  // Q fragments (32 dims each) per column block
+    constexpr int NOB = D / 16;  // 16-dim output blocks
+    static_assert(2 * NLD == 16, "prologue wait counts");
+    __shared__ __attribute__((aligned(1024))) char kb0[C::TILE];
+    __shared__ __attribute__((aligned(1024))) char kb1[C::TILE];
+    __shared__ __attribute__((aligned(1024))) char vb0[C::TILE];
+    __shared__ __attribute__((aligned(1024))) char vb1[C::TILE];
+
+    const int Sq = a.Sq;
+    const float c = a.c;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const int nqt = (Sq + C::BM - 1) / C::BM;
+    int wg = blockIdx.x, split = 0;
+    if constexpr (SPLIT) {
+        split = wg % a.nsplit;
+        wg /= a.nsplit;
+    }
+    const int bh = wg / nqt;
+    const int qt = wg % nqt;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int kv0 = SPLIT ? split * a.split_len : 0;
+    const int Skv = SPLIT ? max(0, min(a.Skv - kv0, a.split_len)) : a.Skv;
+    const T* Qh = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+    const T* Kh = (const T*)a.k + b * a.sk.b + h * a.sk.h + kv0 * a.sk.s;
+    const T* Vh = (const T*)a.v + b * a.sv.b + h * a.sv.h + kv0 * a.sv.s;
+    T* Oh = (T*)a.o + b * a.so.b + h * a.so.h;
+    const long long kss = a.sk.s, vss = a.sv.s;
+    const int qrow0 = qt * C::BM + wave * 32 + i;  // this lane's rows: qrow0 + 16 rb
+    const int ntiles = (Skv + BN - 1) / BN;
+    // Direct loads of tile t of X into dst: one instruction per 1 KB row,
+    // lane l fetching dims 8l..8l+7 of rows wave + 4n. The descriptor covers
+    // the tile's valid rows only (none past the last tile), so the rest read
+    // as zeros.
+    auto issue = [&](const T* X, long long ss, int t, char* dst) __attribute__((always_inline)) {
+        const int rows = min(Skv - t * BN, BN);
+        const int bytes = rows > 0 ? (int)(((rows - 1) * ss + D) * 2) : 0;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(X + (rows > 0 ? t * BN * ss : 0)), 0, bytes, 0x00020000);
+#pragma unroll
+        for (int n = 0; n < NLD; ++n) {
+            const int row = wave + n * C::NW;  // wave-uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)(dst + row * C::KS), 16,
+                                                     lane * 16, (int)(row * ss * 2), 0, 0);
+        }
+    };
+
+    // Q^T fragments (B operands: column = query 16rb + l%16, k = dims
+    // 32s + 8(l/16)..+7).
+    // Issue order K(0), Q, V(0), K(1): the prologue waits for the first two.
+    if (ntiles > 0) issue(Kh, kss, 0, kb0);
+    x8 qf[2][NQF];
+    const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int s = 0; s < NQF; ++s) {
+            const int row = qrow0 + 16 * rb;
+            qf[rb][s] = q_fragment(Qh + row * a.sq.s + 32 * s + 8 * g, row < Sq && ntiles > 0, qneg);
+        }
+    if (ntiles > 0) {
+        issue(Vh, vss, 0, vb0);
+        issue(Kh, kss, 1, kb1);
+    }
+
+    // K read: row 16kb + i, dims 32s + 8g..; V^T read (transposed, per
+    // 16-lane group g): rows 4g + i/4 and 16 + 4g + i/4, dims 16ob + 4(i%4)..
+    const int kbase = i * C::KS + g * 16;
+    const int vbase = (4 * g + (i >> 2)) * C::VS + 8 * (i & 3);
+
+    // S^T = K Q^T of one tile, per column block rb and 16-key block kb, in
+    // two MFMA chains (even and odd Q fragments) added at the end.
+    auto qk = [&](const char* __restrict__ kt, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 Sp[2][2] = {{f32x4{}, f32x4{}}, {f32x4{}, f32x4{}}};
+#pragma unroll
+            for (int s = 0; s < NQF; ++s) {
+                const x8 kf = lds_read16<T>(kt, kbase + kb * 16 * C::KS + s * 64);
+                Sp[0][s & 1] = E::mma16(kf, qf[0][s], Sp[0][s & 1]);
+                Sp[1][s & 1] = E::mma16(kf, qf[1][s], Sp[1][s & 1]);
+            }
+            S[0][kb] = Sp[0][0] + Sp[0][1];
+            S[1][kb] = Sp[1][0] + Sp[1][1];
+        }
+    };
+
+    // The last tile's keys past Skv score -inf.
+    auto mask_tail = [&](int t, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t * BN + kb * 16 + 4 * g + r >= Skv) S[rb][kb][r] = -INFINITY;
+    };
+
+    // P of one column block from its two score blocks, with running max
+    // -nm; pm tracks the largest p and lsum sums the rounded p.
+    auto make_p = [&](const f32x4 (&S)[2], x8& P, float nm, float& lsum, f32x2& pm)
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const f32x4& Sb = S[u >> 1];
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1)], c, nm));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(Sb[2 * (u & 1) + 1], c, nm));
+            const auto hp = E::cvt2(p0, p1);
+            P[2 * u] = hp[0];
+            P[2 * u + 1] = hp[1];
+            lsum = E::sum2(hp, lsum);
+            pm[u & 1] = max3(pm[u & 1], p0, p1);
+        }
+    };
+
+    f32x4 oacc[2][NOB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) {
+            oacc[rb][ob] = f32x4{};
+            agpr_fence2(oacc[rb][ob]);
+        }
+    // Running max (log2 units; finite, so masked keys give p = 0) and row sum.
+    float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+
+    f32x4 S[2][2];  // scores of the tile the next iteration turns into P
+    // Iteration t: scores S of tile t in registers; K(t+1) in kc, V(t) in vc;
+    // K(t+2) loads into kf and V(t+1) into vf.
+    auto iter = [&](int t, char* __restrict__ kf, const char* __restrict__ kc,
+                    const char* __restrict__ vc, char* __restrict__ vf) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's K(t+1) and V(t) rows
+        lds_barrier();                      // ... every wave's; K(t) and V(t-1) buffers free
+        issue(Kh, kss, t + 2, kf);
+        issue(Vh, vss, t + 1, vf);
+        x8 P[2];
+        float lt[2] = {0.f, 0.f};
+        f32x2 pm[2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) make_p(S[rb], P[rb], -m_run[rb], lt[rb], pm[rb]);
+        const bool up0 = __any(!(fmaxf(pm[0][0], pm[0][1]) <= kPmaxLimit));
+        const bool up1 = __any(!(fmaxf(pm[1][0], pm[1][1]) <= kPmaxLimit));
+        f32x4 Sn[2][2];
+        qk(kc, Sn);
+        if (__builtin_expect(up0 || up1, 0)) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                if (rb == 0 ? !up0 : !up1) continue;
+                // The exact max of the tile's rows; O, l and P follow.
+                float mx = fmaxf(max3(S[rb][0][0], S[rb][0][1], S[rb][0][2]),
+                                 max3(S[rb][0][3], S[rb][1][0], S[rb][1][1]));
+                mx = quad_group_max(max3(mx, S[rb][1][2], S[rb][1][3])) * c;
+                const float m_new = fmaxf(m_run[rb], mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - m_new);
+#pragma unroll
+                for (int ob = 0; ob < NOB; ob += 4)
+                    agpr_fence24(oacc[rb][ob], oacc[rb][ob + 1], oacc[rb][ob + 2], oacc[rb][ob + 3]);
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob) {
+                    oacc[rb][ob] *= alpha;
+                    agpr_fence2(oacc[rb][ob]);
+                }
+                l_run[rb] *= alpha;
+                m_run[rb] = m_new;
+                lt[rb] = 0.f;
+                f32x2 pm2 = {0.f, 0.f};
+                make_p(S[rb], P[rb], -m_new, lt[rb], pm2);
+            }
+        }
+        l_run[0] += lt[0];
+        l_run[1] += lt[1];
+        // O^T += V^T P^T: one V^T fragment per 16-dim block, two MFMAs.
+        vgpr_fence2(P[0], P[1]);
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) {
+            const x8 vfr = lds_read_tr2<T>(vc, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
+            mma16_agpr<T>(oacc[0][ob], vfr, P[0]);
+            mma16_agpr<T>(oacc[1][ob], vfr, P[1]);
+        }
+        if ((t + 2) * BN > Skv) mask_tail(t + 1, Sn);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) S[rb][kb] = Sn[rb][kb];
+    };
+
+    if (ntiles > 0) {
+        // Prologue: this wave's K(0) rows and Q have landed once at most the
+        // 16 loads of V(0) and K(1) are in flight; then every wave's. Scores
+        // of tile 0 and their exact max.
+        __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+        lds_barrier();
+        qk(kb0, S);
+        if (BN > Skv) mask_tail(0, S);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const float mx = fmaxf(max3(S[rb][0][0], S[rb][0][1], S[rb][0][2]),
+                                   max3(S[rb][0][3], S[rb][1][0], S[rb][1][1]));
+            m_run[rb] = quad_group_max(max3(mx, S[rb][1][2], S[rb][1][3])) * c;
+        }
+        for (int t = 0; t < ntiles; t += 2) {
+            iter(t, kb0, kb1, vb0, vb1);
+            if (t + 1 < ntiles) iter(t + 1, kb1, kb0, vb1, vb0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the (empty) loads past the end
+    }
+
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int ob = 0; ob < NOB; ob += 4)
+            agpr_fence24(oacc[rb][ob], oacc[rb][ob + 1], oacc[rb][ob + 2], oacc[rb][ob + 3]);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int qrow = qrow0 + 16 * rb;
+        const float l = quad_group_sum(l_run[rb]);
+        if constexpr (SPLIT) {  // unnormalised O and (m, l) of this key range
+            if (qrow < Sq) {
+                const long long r = ((long long)split * a.BH + bh) * Sq + qrow;
+                float* wo = a.ws_o + r * D;
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob)
+                    *reinterpret_cast<f32x4*>(wo + 16 * ob + 4 * g) = oacc[rb][ob];
+                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m_run[rb], l};
+            }
+        } else {
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+            if (qrow < Sq) {
+                T* op = Oh + qrow * a.so.s;
+#pragma unroll
+                for (int ob = 0; ob < NOB; ++ob) {
+                    const auto h0 = E::cvt2(oacc[rb][ob][0] * inv, oacc[rb][ob][1] * inv);
+                    const auto h1 = E::cvt2(oacc[rb][ob][2] * inv, oacc[rb][ob][3] * inv);
+                    *reinterpret_cast<typename E::x4*>(op + 16 * ob + 4 * g) =
+                        typename E::x4{h0[0], h0[1], h1[0], h1[1]};
+                }
+            }
+        }
+    }
+#endif
+}
+
 // Merge of the split key ranges: per output row, with m* the largest
 // running max of its splits and w_s = exp2(m_s - m*),
 //     o = sum_s w_s O_s / sum_s w_s l_s
@@ -1481,6 +1800,14 @@ long long kvres_grid(const KArgs& a) {
     return items >= cus && ntiles % 4 ? cus : 0;
 }
 
+// D = 512 with row-contiguous K/V runs attn_fwd_d512w (32 rows per wave);
+// GFX906_AMD_ATTN_D512W=0 selects attn_fwd_d512 (16 rows per wave) instead,
+// for tests (the two are bit-identical).
+bool d512_wide() {
+    const char* env = getenv("GFX906_AMD_ATTN_D512W");
+    return !(env && env[0] == '0' && env[1] == 0);
+}
+
 template <class T, bool SPLIT>
 void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
     const int D = a.D;
@@ -1488,6 +1815,8 @@ void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
         dim3 grid((unsigned)((a.Sq + Cfg512::BM - 1) / Cfg512::BM) * nwg);
         if (tl)
             hipLaunchKernelGGL((attn_fwd_d512<T, true, SPLIT>), grid, dim3(Cfg512::NT), 0, s, a);
+        else if (d512_wide())
+            hipLaunchKernelGGL((attn_fwd_d512w<T, SPLIT>), grid, dim3(Cfg512W::NT), 0, s, a);
         else
             hipLaunchKernelGGL((attn_fwd_d512<T, false, SPLIT>), grid, dim3(Cfg512::NT), 0, s, a);
     } else if (D == 128) {
