@@ -164,23 +164,42 @@ struct Elem<bf16> {
 // its 256 accumulator registers fill the AGPR file, and the 128 registers of
 // Q and the score accumulators must stay in VGPRs, a split the compiler's
 // own register assignment does not find. The instruction is therefore
-// written out, and the wait states the compiler inserts around MFMAs it
-// knows of are provided by agpr_fence / vgpr_fence around its operands:
-//  * a VALU write of srcB (P) or of the accumulator (initialisation,
-//    rescale) needs 2 wait states before the MFMA reads it;
-//  * a VALU read of the accumulator needs the MFMA to have completed: the
-//    fence before the epilogue (and the rare rescale) gives 24.
-// Every such producer-consumer pair passes through a fence by data
-// dependence, so the fences hold whatever order the scheduler picks; the
-// MFMA's srcA (V from LDS) is ordered by the compiler's lgkmcnt waits, which
-// cover inline-asm operands.
-template <class T>
+// written out, and with it the wait states the compiler's hazard recognizer
+// inserts around MFMAs it knows of (it does not look into asm):
+//  * a VALU write of an operand (P, O at initialisation or after a rescale)
+//    needs 2 wait states before the MFMA reads it: agpr_fence2 and
+//    vgpr_fence2 below follow those writes, tied to them by data dependence;
+//  * a VALU read or write of an MFMA's accumulator registers (the rescale,
+//    the epilogue, copies the register allocator places at block
+//    boundaries) needs the MFMA to have completed (12 wait states on gfx950
+//    for an 8-pass MFMA, 20 for 16 passes): the last MFMA of every tile
+//    carries 24 wait states (DRAIN), ahead of the rescale, the epilogue and
+//    any copy the register allocator places at the loop's edges (draining
+//    only after the last tile instead makes the allocator split O's live
+//    ranges around the two forms, with copies right after MFMAs). The asm
+//    statements are volatile, so nothing moves between an MFMA and that
+//    delay.
+// The MFMA's srcA (V from LDS) is ordered by the compiler's lgkmcnt waits,
+// which cover inline-asm operands. tests/test_d512w_hazards.py checks the
+// compiled kernel for both rules. The fences also tie O (and P) to AGPRs
+// (VGPRs) where the kernel's own VALU work touches them, which keeps the
+// register allocator from giving O VGPR homes there (it spills otherwise).
+template <class T, bool DRAIN = false>
 __device__ __forceinline__ void mma16_agpr(f32x4& acc, typename Elem<T>::x8 a,
                                            typename Elem<T>::x8 b) {
-    if constexpr (std::is_same<T, f16>::value)
-        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-    else
-        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    if constexpr (std::is_same<T, f16>::value) {
+        if constexpr (DRAIN)
+            asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(acc) : "v"(a), "v"(b));
+        else
+            asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    } else {
+        if constexpr (DRAIN)
+            asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(acc) : "v"(a), "v"(b));
+        else
+            asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    }
 }
 // 2 wait states after a VALU write, before an MFMA reads the registers.
 __device__ __forceinline__ void agpr_fence2(f32x4& x) { asm("s_nop 1" : "+a"(x)); }
@@ -1479,13 +1498,19 @@ attn_fwd_d512w(const KArgs a) {
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    int wg = blockIdx.x, split = 0;
+    // Workgroup w runs on XCD w % 8 (the dispatcher deals workgroups to the
+    // eight XCDs in turn). When the grid divides by 8, consecutive work items
+    // go to one XCD, and work items enumerate the query tiles of one K/V range
+    // (head, split) consecutively: an XCD's L2 then streams the K/V of as few
+    // heads as possible, each tile once for all its workgroups.
+    int w = blockIdx.x;
+    if ((gridDim.x & 7) == 0) w = (w & 7) * (int)(gridDim.x >> 3) + (w >> 3);
+    const int qt = w % nqt;
+    int bh = w / nqt, split = 0;
     if constexpr (SPLIT) {
-        split = wg % a.nsplit;
-        wg /= a.nsplit;
+        split = bh % a.nsplit;
+        bh /= a.nsplit;
     }
-    const int bh = wg / nqt;
-    const int qt = wg % nqt;
     const int b = bh / a.H, h = bh - b * a.H;
     const int kv0 = SPLIT ? split * a.split_len : 0;
     const int Skv = SPLIT ? max(0, min(a.Skv - kv0, a.split_len)) : a.Skv;
@@ -1538,30 +1563,50 @@ attn_fwd_d512w(const KArgs a) {
 
     // S^T = K Q^T of one tile, per column block rb and 16-key block kb, in
     // two MFMA chains (even and odd Q fragments) added at the end.
+    // K fragments in flight in the QK^T step: each read is issued six
+    // fragments (12 MFMAs, about 190 cycles) ahead of its use, which covers
+    // the LDS latency a single wave per SIMD cannot hide otherwise
+    // (measured on MI355X against 2, 4, 8 and 10 in flight). The softmax
+    // VALU work of the same basic block is left to the scheduler: pinning it
+    // between the MFMAs or ahead of them was measured slower.
+    constexpr int NKQ = 6;
     auto qk = [&](const char* __restrict__ kt, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+        constexpr int NF = 2 * NQF;  // fragments: 16 per 16-key block
+        auto kread = [&](int f) __attribute__((always_inline)) {
+            return lds_read16<T>(kt, kbase + (f / NQF) * 16 * C::KS + (f % NQF) * 64);
+        };
+        x8 kq[NKQ];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x4 Sp[2][2] = {{f32x4{}, f32x4{}}, {f32x4{}, f32x4{}}};
+        for (int j = 0; j < NKQ; ++j) kq[j] = kread(j);
+        f32x4 Sp[2][2];
 #pragma unroll
-            for (int s = 0; s < NQF; ++s) {
-                const x8 kf = lds_read16<T>(kt, kbase + kb * 16 * C::KS + s * 64);
-                Sp[0][s & 1] = E::mma16(kf, qf[0][s], Sp[0][s & 1]);
-                Sp[1][s & 1] = E::mma16(kf, qf[1][s], Sp[1][s & 1]);
+        for (int f = 0; f < NF; ++f) {
+            const int kb = f / NQF, s = f % NQF;
+            if (s == 0) Sp[0][0] = Sp[0][1] = Sp[1][0] = Sp[1][1] = f32x4{};
+            const x8 kf = kq[f % NKQ];
+            if (f + NKQ < NF) kq[f % NKQ] = kread(f + NKQ);
+            Sp[0][s & 1] = E::mma16(kf, qf[0][s], Sp[0][s & 1]);
+            Sp[1][s & 1] = E::mma16(kf, qf[1][s], Sp[1][s & 1]);
+            if (s == NQF - 1) {
+                S[0][kb] = Sp[0][0] + Sp[0][1];
+                S[1][kb] = Sp[1][0] + Sp[1][1];
             }
-            S[0][kb] = Sp[0][0] + Sp[0][1];
-            S[1][kb] = Sp[1][0] + Sp[1][1];
         }
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, NKQ, 0);
+#pragma unroll
+        for (int f = 0; f < NF - NKQ; ++f) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 2 * NKQ, 0);
     };
 
-    // The last tile's keys past Skv score -inf.
-    auto mask_tail = [&](int t, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (t * BN + kb * 16 + 4 * g + r >= Skv) S[rb][kb][r] = -INFINITY;
+    // V^T fragment of 16-dim block ob.
+    // V^T fragments in flight in the PV step (two transposed reads each; 8
+    // measured best against 4 and 6).
+    constexpr int NVQ = 8;
+    auto vread = [&](const char* vt, int ob) __attribute__((always_inline)) {
+        return lds_read_tr2<T>(vt, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
     };
 
     // P of one column block from its two score blocks, with running max
@@ -1592,9 +1637,24 @@ attn_fwd_d512w(const KArgs a) {
     // Running max (log2 units; finite, so masked keys give p = 0) and row sum.
     float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
 
+    // The last tile's keys past Skv score -inf.
+    auto mask_tail = [&](int t, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t * BN + kb * 16 + 4 * g + r >= Skv) S[rb][kb][r] = -INFINITY;
+    };
+
     f32x4 S[2][2];  // scores of the tile the next iteration turns into P
     // Iteration t: scores S of tile t in registers; K(t+1) in kc, V(t) in vc;
-    // K(t+2) loads into kf and V(t+1) into vf.
+    // K(t+2) loads into kf and V(t+1) into vf. P of tile t and the QK^T
+    // MFMAs of tile t+1 share a basic block; the rescale test of tile t (a
+    // rare branch) follows, then the PV MFMAs of tile t. Interleaving the
+    // softmax VALU work with the PV MFMAs instead (a single wave per SIMD
+    // issues both) was measured 3 % slower.
     auto iter = [&](int t, char* __restrict__ kf, const char* __restrict__ kc,
                     const char* __restrict__ vc, char* __restrict__ vf) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's K(t+1) and V(t) rows
@@ -1610,6 +1670,11 @@ attn_fwd_d512w(const KArgs a) {
         const bool up1 = __any(!(fmaxf(pm[1][0], pm[1][1]) <= kPmaxLimit));
         f32x4 Sn[2][2];
         qk(kc, Sn);
+        // The first V^T fragments, read before the rare-path branch so that
+        // their LDS latency overlaps it.
+        x8 vq[NVQ];
+#pragma unroll
+        for (int j = 0; j < NVQ; ++j) vq[j] = vread(vc, j);
         if (__builtin_expect(up0 || up1, 0)) {
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -1637,13 +1702,19 @@ attn_fwd_d512w(const KArgs a) {
         }
         l_run[0] += lt[0];
         l_run[1] += lt[1];
-        // O^T += V^T P^T: one V^T fragment per 16-dim block, two MFMAs.
+        // O^T += V^T P^T: one V^T fragment per 16-dim block, two MFMAs, with
+        // NVQ fragments in flight (the MFMAs are volatile asm, so the LDS
+        // reads keep their place in this order).
         vgpr_fence2(P[0], P[1]);
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) {
-            const x8 vfr = lds_read_tr2<T>(vc, vbase + 32 * ob, vbase + 32 * ob + 16 * C::VS);
+            const x8 vfr = vq[ob % NVQ];
+            if (ob + NVQ < NOB) vq[ob % NVQ] = vread(vc, ob + NVQ);
             mma16_agpr<T>(oacc[0][ob], vfr, P[0]);
-            mma16_agpr<T>(oacc[1][ob], vfr, P[1]);
+            if (ob + 1 < NOB)
+                mma16_agpr<T>(oacc[1][ob], vfr, P[1]);
+            else
+                mma16_agpr<T, true>(oacc[1][ob], vfr, P[1]);
         }
         if ((t + 2) * BN > Skv) mask_tail(t + 1, Sn);
 #pragma unroll
