@@ -472,13 +472,18 @@ attn_fwd_pipe(const KArgs a) {
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int nqt = (Sq + C::BM - 1) / C::BM;
-    int wg = blockIdx.x, split = 0;
+    // Work item w = (head, key split, query tile), query tiles consecutive;
+    // consecutive items go to one XCD when the grid divides by 8 (the
+    // dispatcher deals workgroup w to XCD w % 8), so an XCD's L2 streams the
+    // K/V of as few heads as possible (c2 +2 %).
+    int w = blockIdx.x;
+    if ((gridDim.x & 7) == 0) w = (w & 7) * (int)(gridDim.x >> 3) + (w >> 3);
+    const int qt = w % nqt;
+    int bh = w / nqt, split = 0;
     if constexpr (SPLIT) {
-        split = wg % a.nsplit;
-        wg /= a.nsplit;
+        split = bh % a.nsplit;
+        bh /= a.nsplit;
     }
-    const int bh = wg / nqt;
-    const int qt = wg % nqt;
     const int b = bh / a.H, h = bh - b * a.H;
     // This workgroup's keys: [kv0, kv0 + Skv) of the head.
     const int kv0 = SPLIT ? split * a.split_len : 0;
