@@ -669,13 +669,13 @@ attn_fwd_pipe(const KArgs a) {
                     }
                 }
             } else {
-                const float lm0 = lane_max(S, 0), lm1 = lane_max(S, 1);
-                if (__any(lm0 > m_run[0] || lm1 > m_run[1])) {
-                    const float lm[2] = {lm0, lm1};
+                // Each column block moves only when one of its queries' max
+                // rose (+0.8 % c3 against moving both together).
+                const float lm[2] = {lane_max(S, 0), lane_max(S, 1)};
 #pragma unroll
-                    for (int nb = 0; nb < 2; ++nb)
+                for (int nb = 0; nb < 2; ++nb)
+                    if (__any(lm[nb] > m_run[nb]))
                         rescale(nb, max2(m_run[nb], quad_group_max(lm[nb])));
-                }
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
                     block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, lp[nb]);
@@ -969,11 +969,10 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
         return max2(max3(mx, S[1][nb][2], S[1][nb][3]), my);
     };
     auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
-        const float lm0 = lane_max(S, 0), lm1 = lane_max(S, 1);
-        if (__any(lm0 > m_run[0] || lm1 > m_run[1])) {
-            const float lm[2] = {lm0, lm1};
+        const float lm[2] = {lane_max(S, 0), lane_max(S, 1)};
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
+        for (int nb = 0; nb < 2; ++nb) {
+            if (__any(lm[nb] > m_run[nb])) {
                 const float m_new = max2(m_run[nb], quad_group_max(lm[nb]));
                 const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
 #pragma unroll
