@@ -41,8 +41,12 @@ CONV_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3d_vae_kernel_trace.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # Defaults: 30 untimed launches (about 55 ms of the north star) let the
+    # card settle its clock under sustained matrix load (it climbs from about
+    # 1.5 to 1.87 GHz over the first tens of milliseconds, then holds), so
+    # the 50 timed launches measure the steady state a model's layers run in.
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload", default="ns",
                     choices=["ns", "ns_h8", "c1", "c2", "c3", "c4", "c5", "conv3d_vae"],
