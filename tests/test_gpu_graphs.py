@@ -41,7 +41,10 @@ def replay_and_check(fn, out, expect, replays=3):
 
 @pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 8, 1024, 1024, 128),   # whole grid
                                           (1, 1, 200, 3000, 64),     # split key ranges
-                                          (2, 3, 77, 129, 40)])      # padded head dim
+                                          (2, 3, 77, 129, 40),       # padded head dim
+                                          (2, 16, 4096, 77, 64),     # K/V-resident kernel
+                                          (1, 8, 4096, 256, 512),    # D = 512, 32 rows/wave
+                                          (1, 2, 300, 700, 512)])    # D = 512, split
 def test_attention_graph_replays(B, H, Sq, Skv, D):
     q, k, v = (t.to(DEV) for t in make_inputs(B, H, Sq, Skv, D, 1.0, 1.0, seed=Sq + Skv))
     expect = gfx906_amd.attn(q, k, v, D ** -0.5)
