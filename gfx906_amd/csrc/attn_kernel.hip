@@ -392,9 +392,11 @@ template <class C, class T>
 __device__ __forceinline__ void issue_tile(const T* __restrict__ X, int n0, int Skv, int D,
                                            long long ss, char* stage, int wave,
                                            const int (&off)[C::BLKS / C::NW]) {
-    const int rows = max(0, min(Skv - n0, C::BN));
-    // Uniform; readfirstlane keeps the descriptor in SGPRs (a clamp selected
-    // as a VALU op would otherwise force a waterfall loop around each load).
+    // Uniform; written as a min and a select (scalar instructions) rather than
+    // a clamp, which is selected as a vector med3 and then needs a
+    // readfirstlane; readfirstlane keeps the descriptor in SGPRs either way (a
+    // VGPR descriptor would force a waterfall loop around each load).
+    const int rows = min(Skv - n0, C::BN);
     const int bytes =
         __builtin_amdgcn_readfirstlane(rows > 0 ? (int)(((rows - 1) * ss + D) * 2) : 0);
     const __amdgpu_buffer_rsrc_t r =
@@ -461,10 +463,16 @@ attn_fwd_pipe(const KArgs a) {
     constexpr int LPT = C::BLKS / C::NW;  // loads per wave per K (or V) tile
     static_assert(2 * LPT < 16, "vmcnt immediate");
     constexpr int kWaitNext = 0x0F70 | (2 * LPT);  // vmcnt(one tile of loads)
-    __shared__ __attribute__((aligned(1024))) char st0[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) char st1[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) char st2[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) char st3[C::STAGE];
+    // The ring: K and V tiles of stage s in ks and vs, eight separate arrays
+    // (the compiler then tells loads into one from reads of another apart).
+    __shared__ __attribute__((aligned(1024))) char k0[TILE];
+    __shared__ __attribute__((aligned(1024))) char k1[TILE];
+    __shared__ __attribute__((aligned(1024))) char k2[TILE];
+    __shared__ __attribute__((aligned(1024))) char k3[TILE];
+    __shared__ __attribute__((aligned(1024))) char v0[TILE];
+    __shared__ __attribute__((aligned(1024))) char v1[TILE];
+    __shared__ __attribute__((aligned(1024))) char v2[TILE];
+    __shared__ __attribute__((aligned(1024))) char v3[TILE];
 
     const int Sq = a.Sq, D = a.D;
     const float c = a.c;
@@ -545,9 +553,9 @@ attn_fwd_pipe(const KArgs a) {
     if (ntiles > 0) {
         int koff[LPT], voff[LPT];
         tile_offsets<C, PAD>(koff, voff, D, (int)a.sk.s, (int)a.sv.s, wave, lane);
-        auto issue = [&](int t, char* dst) __attribute__((always_inline)) {
-            issue_tile<C>(Kh, t * C::BN, Skv, D, a.sk.s, dst, wave, koff);
-            issue_tile<C>(Vh, t * C::BN, Skv, D, a.sv.s, dst + TILE, wave, voff);
+        auto issue = [&](int t, char* kdst, char* vdst) __attribute__((always_inline)) {
+            issue_tile<C>(Kh, t * C::BN, Skv, D, a.sk.s, kdst, wave, koff);
+            issue_tile<C>(Vh, t * C::BN, Skv, D, a.sv.s, vdst, wave, voff);
         };
         // K (and Q) read: row 16kb + l%16 of a 32-key block, dims 32s + 8(l/16)..
         int kaddr[NQF];
@@ -560,15 +568,23 @@ attn_fwd_pipe(const KArgs a) {
         // 4g + e (+16 for the block's second key half), dims 16ob + 4j..+3, so
         // lane l receives dim 16ob + l%16 of keys 4g..4g+3 (16 + 4g..).
         int vaddr[NOB];
+        constexpr int kVBias = 4 * TILE >= 65536 ? 65536 : 0;
         {
             const int vrow = 4 * g + (i >> 2);
             const int vx = vswz<NU>(vrow) >> 1;
 #pragma unroll
-            for (int ob = 0; ob < NOB; ++ob) vaddr[ob] = vrow * RB + (ob ^ vx) * 32 + (i & 3) * 8;
+            for (int ob = 0; ob < NOB; ++ob) {
+                // Held as vaddr + 64 KiB, opaque to the compiler: the V arrays
+                // follow the 64 KiB of K arrays (D = 128), so every V read then
+                // takes its array's place as an immediate offset from these
+                // registers instead of an address add per read and tile.
+                vaddr[ob] = vrow * RB + (ob ^ vx) * 32 + (i & 3) * 8 + kVBias;
+                asm volatile("" : "+v"(vaddr[ob]));
+            }
         }
 
-        // S^T of 32-key block blk of the tile in stage st.
-        auto qk = [&](const char* st, int blk, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
+        // S^T of 32-key block blk of the K tile kt.
+        auto qk = [&](const char* kt, int blk, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -577,7 +593,7 @@ attn_fwd_pipe(const KArgs a) {
             for (int s = 0; s < NQF; ++s)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const x8 kf = lds_read16<T>(st, kaddr[s] + (32 * blk + 16 * kb) * RB);
+                    const x8 kf = lds_read16<T>(kt, kaddr[s] + (32 * blk + 16 * kb) * RB);
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) S[kb][nb] = E::mma16(kf, qf[nb][s], S[kb][nb]);
                 }
@@ -591,12 +607,11 @@ attn_fwd_pipe(const KArgs a) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
             }
         };
-        // O^T += V^T P^T for 32-key block blk of the tile in stage st.
-        auto pv = [&](const char* st, int blk, const x8 (&P)[2]) __attribute__((always_inline)) {
-            const char* sv = st + TILE;
+        // O^T += V^T P^T for 32-key block blk of the V tile sv.
+        auto pv = [&](const char* sv, int blk, const x8 (&P)[2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) {
-                const int off = vaddr[ob] + 32 * blk * RB;
+                const int off = vaddr[ob] - kVBias + 32 * blk * RB;
                 const x8 vf = lds_read_tr2<T>(sv, off, off + 16 * RB);
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
@@ -692,20 +707,21 @@ attn_fwd_pipe(const KArgs a) {
         Pb[0] = x8{};  // block -1: no keys
         Pb[1] = x8{};
 
-        // Tile w (blocks 2w, 2w+1) in stage cur; prev holds tile w-1, nxt
-        // tile w+1; fill (the stage of tile w-1) takes tile w+3.
-        auto tile = [&](int w, const char* prev, const char* cur, const char* nxt, char* fill)
-                __attribute__((always_inline)) {
+        // Tile w (blocks 2w, 2w+1) in stage cur (K tile kc, V tile vc); vp
+        // holds V of tile w-1, kn K of tile w+1; the stage of tile w-1 (kf,
+        // vf) takes tile w+3.
+        auto tile = [&](int w, const char* vp, const char* kc, const char* vc, const char* kn,
+                        char* kf, char* vf) __attribute__((always_inline)) {
             mask(Sa, w * C::BN);
-            pv(prev, 1, Pb);   // block 2w-1
-            qk(cur, 1, Sb);    // block 2w+1
+            pv(vp, 1, Pb);     // block 2w-1
+            qk(kc, 1, Sb);     // block 2w+1
             softmax(Sa, Pa);   // block 2w
             __builtin_amdgcn_s_waitcnt(kWaitNext);  // own loads of tile w+1 done
             lds_barrier();                          // every wave's; tile w-1 consumed
-            issue(w + 3, fill);
+            issue(w + 3, kf, vf);
             mask(Sb, w * C::BN + 32);
-            pv(cur, 0, Pa);    // block 2w
-            qk(nxt, 0, Sa);    // block 2w+2
+            pv(vc, 0, Pa);     // block 2w
+            qk(kn, 0, Sa);     // block 2w+2
             softmax(Sb, Pb);   // block 2w+1
         };
 
@@ -726,17 +742,18 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
                     issue_tile<C>(Qh, qt * C::BM + m * C::BN, Sq, D, a.sq.s,
-                                  (m < 2 ? st2 : st3) + (m & 1) * TILE, wave, qoff);
+                                  m == 0 ? k2 : m == 1 ? v2 : m == 2 ? k3 : v3, wave, qoff);
             }
         }
-        issue(0, st0);
-        issue(1, st1);
+        issue(0, k0, v0);
+        issue(1, k1, v1);
         if constexpr (!PAD) {
             if (q_lds) {
                 __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * LPT));  // this wave's Q loads landed
                 lds_barrier();                                  // every wave's
                 const char* qsrc =
-                    ((wave >> 2) ? st3 : st2) + ((wave >> 1) & 1) * TILE + (wave & 1) * 32 * RB;
+                    ((wave >> 1) == 0 ? k2 : (wave >> 1) == 1 ? v2 : (wave >> 1) == 2 ? k3 : v3) +
+                    (wave & 1) * 32 * RB;
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -748,23 +765,23 @@ attn_fwd_pipe(const KArgs a) {
             }
         }
         for (int z = tid; z < TILE / 16; z += C::NT)
-            *reinterpret_cast<u32x4*>(st3 + TILE + 16 * z) = u32x4{};
+            *reinterpret_cast<u32x4*>(v3 + 16 * z) = u32x4{};
         __builtin_amdgcn_s_waitcnt(kWaitNext);
         lds_barrier();
-        issue(2, st2);
-        qk(st0, 0, Sa);
+        issue(2, k2, v2);
+        qk(k0, 0, Sa);
 
         // Whole groups of four tiles (tiles past the end hold zeros and are
         // masked to p = 0); a single exit keeps the loop's register
         // allocation intact.
         for (int w0 = 0;; w0 += 4) {
-            tile(w0 + 0, st3, st0, st1, st3);
-            tile(w0 + 1, st0, st1, st2, st0);
-            tile(w0 + 2, st1, st2, st3, st1);
-            tile(w0 + 3, st2, st3, st0, st2);
+            tile(w0 + 0, v3, k0, v0, k1, k3, v3);
+            tile(w0 + 1, v0, k1, v1, k2, k0, v0);
+            tile(w0 + 2, v1, k2, v2, k3, k1, v1);
+            tile(w0 + 3, v2, k3, v3, k0, k2, v2);
             if (w0 + 4 >= ntiles) break;
         }
-        pv(st3, 1, Pb);  // block 2w+1 of the last tile
+        pv(v3, 1, Pb);   // block 2w+1 of the last tile
         // The zero-range loads past the end must land before the workgroup's
         // LDS is released.
         __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -796,10 +813,10 @@ attn_fwd_pipe(const KArgs a) {
         // rows. The barrier makes sure every wave is done with the ring.
         constexpr int RS = DP * 2 + 16;   // staging row stride, bytes
         constexpr int CPR = DP * 2 / 16;  // 16-byte pieces per row
-        static_assert(2 * 32 * RS <= C::STAGE, "two waves' staging per ring stage");
+        static_assert(32 * RS <= TILE, "a wave's staging per ring array");
         lds_barrier();
-        char* const sa = (wave >> 1) == 0 ? st0 : (wave >> 1) == 1 ? st1 : (wave >> 1) == 2 ? st2 : st3;
-        char* const stg = sa + (wave & 1) * 32 * RS;
+        char* const stg = wave == 0 ? k0 : wave == 1 ? k1 : wave == 2 ? k2 : wave == 3 ? k3 :
+                          wave == 4 ? v0 : wave == 5 ? v1 : wave == 6 ? v2 : v3;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const float l = quad_group_sum(lacc[nb][0]);
