@@ -597,14 +597,19 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) S[kb][nb] = E::mma16(kf, qf[nb][s], S[kb][nb]);
                 }
-            if constexpr (DP == 64) {  // K reads interleaved with the MFMAs (+2 % c5)
-                __builtin_amdgcn_sched_group_barrier(kSgDsRead, 3, 0);
+            // K reads interleaved with the MFMAs: A fragments ahead, then one
+            // more per MFMA pair (measured against the compiler's own order:
+            // D = 64 with A = 3, +2 % c5; D = 128 with A = 2, +0.8 % north
+            // star and c2, where A = 1 lost 4 % and A = 3, 4 did not gain).
+            {
+                constexpr int A = DP == 64 ? 3 : 2;
+                __builtin_amdgcn_sched_group_barrier(kSgDsRead, A, 0);
 #pragma unroll
-                for (int n = 0; n < 2 * NQF - 3; ++n) {
+                for (int n = 0; n < 2 * NQF - A; ++n) {
                     __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 2 * A, 0);
             }
         };
         // O^T += V^T P^T for 32-key block blk of the V tile sv.
