@@ -333,9 +333,14 @@ __device__ __forceinline__ int vswz(int r) { return NU >= 16 ? 2 * (r & 7) : 2 *
 // so every stretch of a wave's instruction stream carries matrix and vector
 // work (two blocks of S and of P are live).
 //
-// K/V tiles are 64 keys (two blocks) in a ring of four LDS stages, separate
-// arrays so that the compiler can tell their accesses apart (a read of one
-// stage then never waits for loads into another). The barrier that opens
+// K/V tiles are 64 keys (two blocks) in a ring of four LDS stages, each
+// stage's K and V tiles separate arrays, so that the compiler can tell their
+// accesses apart (a read of one array then never waits for loads into
+// another), with the four K arrays first: for D = 128 every K read then
+// reaches its array through the 16-bit immediate offset of one address
+// register, and every V read through one register that holds its address
+// plus 64 KiB (no address arithmetic in the loop: NS +1.7 %, c2 +1.7 %,
+// together with a scalar clamp of the tile rows). The barrier that opens
 // tile w+1 follows the iteration that finished every read of tile w-1, whose
 // stage then takes tile w+3: loads run two tiles ahead. Tiles past the end
 // are loaded anyway, as zeros (empty buffer range), which keeps every wait
@@ -352,7 +357,6 @@ struct Cfg {
     static constexpr int NU = DP / 8;           // 16-byte units per row
     static constexpr int RB = DP * 2;           // bytes per LDS row
     static constexpr int TILE = BN * RB;        // bytes of one K (or V) tile
-    static constexpr int STAGE = 2 * TILE;      // K tile, then V tile
     static constexpr int BLKS = TILE / 1024;    // 1 KB direct-load blocks per tile
     static_assert(BLKS % NW == 0, "tile must split evenly over waves");
     static_assert(DP % 32 == 0 && DP <= 128, "head-dim class");

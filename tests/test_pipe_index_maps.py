@@ -166,6 +166,7 @@ def test_planted_swizzle_mistake_conflicts():
 @pytest.mark.parametrize("dp", [64, 128])
 def test_staged_output_covers_each_element_once(dp):
     rs, cpr = dp * 2 + 16, dp * 2 // 16
+    assert 32 * rs <= 64 * dp * 2  # a wave's staging fits one ring array (a 64-key tile)
     written = {}
     for nb in range(2):
         for ob in range(dp // 16):
