@@ -587,6 +587,9 @@ attn_fwd_pipe(const KArgs a) {
             }
         }
 
+        // PV MFMAs left to the QK^T step that follows (see pv; for D = 64,
+        // 2 and 4 measured -0.5 and -1.2 % on c5).
+        constexpr int kPvTail = DP == 128 ? 4 : 0;
         // S^T of 32-key block blk of the K tile kt.
         auto qk = [&](const char* kt, int blk, f32x4 (&S)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -605,9 +608,12 @@ attn_fwd_pipe(const KArgs a) {
             // more per MFMA pair (measured against the compiler's own order:
             // D = 64 with A = 3, +2 % c5; D = 128 with A = 2, +0.8 % north
             // star and c2, where A = 1 lost 4 % and A = 3, 4 did not gain).
+            // The first A reads go out while the last kPvTail MFMAs of the
+            // PV step before are still to issue (see pv).
             {
                 constexpr int A = DP == 64 ? 3 : 2;
                 __builtin_amdgcn_sched_group_barrier(kSgDsRead, A, 0);
+                if constexpr (kPvTail > 0) __builtin_amdgcn_sched_group_barrier(kSgMfma, kPvTail, 0);
 #pragma unroll
                 for (int n = 0; n < 2 * NQF - A; ++n) {
                     __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
@@ -628,14 +634,17 @@ attn_fwd_pipe(const KArgs a) {
 
             // Three V fragments ahead of the MFMAs that use them, then one
             // more per MFMA pair (measured: +4 % north star against the
-            // compiler's own order).
+            // compiler's own order). Every PV step is followed by a QK^T step,
+            // whose first K reads are placed ahead of this step's last
+            // kPvTail MFMAs (D = 128: +1.2 % north star and c2 with 4 or 6,
+            // -5 % with 8, which also holds back QK^T MFMAs).
             __builtin_amdgcn_sched_group_barrier(kSgDsRead, 6, 0);
 #pragma unroll
             for (int n = 0; n < NOB - 3; ++n) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(kSgMfma, 6, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 6 - kPvTail, 0);
         };
         // Scores of keys >= Skv (block keys key0..key0+31) to -inf, for the
         // last one or two blocks only.
