@@ -2,6 +2,7 @@
 and the figures it reads from the committed rocprofv3 summary."""
 
 import os
+import re
 import subprocess
 import sys
 
@@ -18,13 +19,29 @@ def test_more_than_one_gpu_is_refused():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
+def _scaled_bytes(text, what):
+    """The '<what> = N KiB * 1024 * f = B B' line of the summary, checked."""
+    m = re.search(rf"^\s*{what}\s*=\s*([\d,.]+) KiB \* 1024 \* ([\d.]+)\s*=\s*([\d,]+) B",
+                  text, re.M)
+    assert m, what
+    kib, factor, total = (float(m.group(1).replace(",", "")), float(m.group(2)),
+                          int(m.group(3).replace(",", "")))
+    assert abs(kib * 1024 * factor - total) <= 0.5e-4 * total
+    return total
+
+
 def test_profile_figures_match_the_committed_summary():
     text = open(bench.TRAFFIC_FILE).read()
     fig = bench.read_profile_figures()
     # the summary states the scaled read and write bytes it adds up
-    assert fig["traffic"] == 335824365 + 67108864
+    read, write = _scaled_bytes(text, "read"), _scaled_bytes(text, "write")
+    assert fig["traffic"] == read + write
     assert f"hbm_bytes_per_launch: {int(fig['traffic'])}" in text
-    assert fig["mfma_busy_pct"] == 61.9 and fig["lds_bank_conflict_pct"] == 0.29
+    # O (16 heads x 16384 rows x 128 dims fp16) is written exactly once
+    assert write == 16 * 16384 * 128 * 2
+    # reads: at least Q, K and V once
+    assert read >= 3 * 16 * 16384 * 128 * 2
+    assert 40 < fig["mfma_busy_pct"] < 100 and 0 <= fig["lds_bank_conflict_pct"] < 5
     # the counters name the workload they were measured on
     assert fig["counters_workload"].startswith("ns_h8 (B1 H8 Sq=Skv=16384 D128")
 
