@@ -288,30 +288,31 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
 
 // Whether some element of a block's rounded P (two 8-element operands, all
 // non-negative) exceeds `lim` or is NaN, in any lane of the wave. The first
-// block (running max -1e30, p = inf) always does. fp16: a tree of
-// v_pk_maximum3_f16 over the eight packed registers. bf16 (no packed bf16
-// maximum): non-negative bf16 values order as their 16-bit patterns, so a
-// tree of packed unsigned 16-bit maxima (NaN patterns sort above inf).
+// block (running max -1e30, p = inf) always does. A tree of
+// v_pk_maximum3_f16 over the eight packed registers (4 instructions), then
+// one compare per half. bf16 has no packed maximum; its registers go
+// through the same tree read as fp16: non-negative values of either type
+// order as their 16-bit patterns, so the fp16 maximum of the patterns is the
+// pattern of the bf16 maximum, compared with the limit's bf16 pattern read as
+// fp16 (7.0 for 2^15). A bf16 inf or NaN reads as an fp16 NaN, which the
+// maximum propagates and the compare flags, as it does every pattern above
+// the limit's. (Seven packed 16-bit integer maxima before: bit-identical
+// decisions, three more instructions per block.)
 template <class T>
 __device__ __forceinline__ bool p_above(const typename Elem<T>::x8 (&P)[2], float lim) {
     const u32x4 a = __builtin_bit_cast(u32x4, P[0]), b = __builtin_bit_cast(u32x4, P[1]);
-    if constexpr (std::is_same<T, f16>::value) {
-        auto h = [](unsigned u) { return __builtin_bit_cast(f16x2, u); };
-        auto mx = [](f16x2 x, f16x2 y) { return __builtin_elementwise_maximum(x, y); };
-        const f16x2 x = mx(mx(h(a[0]), h(a[1])), h(a[2]));
-        const f16x2 y = mx(mx(h(a[3]), h(b[0])), h(b[1]));
-        const f16x2 z = mx(mx(h(b[2]), h(b[3])), x);
-        const f16x2 r = mx(y, z);
-        return __any(!(r[0] <= (f16)lim) || !(r[1] <= (f16)lim));
-    } else {
-        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-        auto u = [](unsigned w) { return __builtin_bit_cast(u16x2, w); };
-        auto mx = [](u16x2 x, u16x2 y) { return __builtin_elementwise_max(x, y); };
-        const u16x2 r = mx(mx(mx(u(a[0]), u(a[1])), mx(u(a[2]), u(a[3]))),
-                           mx(mx(u(b[0]), u(b[1])), mx(u(b[2]), u(b[3]))));
-        const unsigned short lb = __builtin_bit_cast(unsigned short, (bf16)lim);
-        return __any(max(r[0], r[1]) > lb);
-    }
+    auto h = [](unsigned u) { return __builtin_bit_cast(f16x2, u); };
+    auto mx = [](f16x2 x, f16x2 y) { return __builtin_elementwise_maximum(x, y); };
+    const f16x2 x = mx(mx(h(a[0]), h(a[1])), h(a[2]));
+    const f16x2 y = mx(mx(h(a[3]), h(b[0])), h(b[1]));
+    const f16x2 z = mx(mx(h(b[2]), h(b[3])), x);
+    const f16x2 r = mx(y, z);
+    f16 lh;
+    if constexpr (std::is_same<T, f16>::value)
+        lh = (f16)lim;
+    else
+        lh = __builtin_bit_cast(f16, (bf16)lim);
+    return __any(!(r[0] <= lh) || !(r[1] <= lh));
 }
 #endif
 
