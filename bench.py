@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import re
 import sys
@@ -36,17 +37,22 @@ WORKLOAD = dict(B=1, H=16, Sq=16384, Skv=16384, D=128)
 SEED = 106
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_pmc.txt")
 CONV_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3d_vae_kernel_trace.txt")
+WARMUP_MS = 250.0  # default warm-up: about this much back-to-back work ...
+MIN_WARMUP = 30  # ... and at least this many launches
+MAX_WARMUP = 20000
 
 
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # Defaults: 30 untimed launches (about 55 ms of the north star) let the
-    # card settle its clock under sustained matrix load (it climbs from about
-    # 1.5 to 1.87 GHz over the first tens of milliseconds, then holds), so
-    # the 50 timed launches measure the steady state a model's layers run in.
+    # The card climbs from about 1.5 to 1.87 GHz over the first tens of
+    # milliseconds of sustained matrix load, then holds. Without --warmup,
+    # the untimed launches run for about WARMUP_MS of back-to-back work (at
+    # least MIN_WARMUP launches), so the 50 timed launches measure the steady
+    # state a model's layers run in whatever the kernel's length; an explicit
+    # --warmup W runs exactly W.
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload", default="ns",
                     choices=["ns", "ns_h8", "c1", "c2", "c3", "c4", "c5", "conv3d_vae"],
@@ -61,6 +67,32 @@ def parse_args():
                     help="instead of attention, time a plain device copy of this many bytes "
                          "(reference point for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def warm_up(call, requested):
+    """Runs the untimed launches and returns how many ran: exactly
+    ``requested`` when given, else enough for about WARMUP_MS of back-to-back
+    launches (sized by the host time of one synchronised launch, which
+    over-counts short kernels' length and so errs towards fewer), at least
+    MIN_WARMUP and at most MAX_WARMUP."""
+    import torch
+
+    if requested is not None:
+        for _ in range(requested):
+            call()
+        torch.cuda.synchronize()
+        return requested
+    call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    call()
+    torch.cuda.synchronize()
+    one = max(time.perf_counter() - t0, 1e-6)
+    n = min(MAX_WARMUP, max(MIN_WARMUP, math.ceil(WARMUP_MS * 1e-3 / one)))
+    for _ in range(n - 2):
+        call()
+    torch.cuda.synchronize()
+    return n
 
 
 def copy_calibration(nbytes, steps):
@@ -162,9 +194,7 @@ def conv3d_bench(args):
     def call():
         conv(x, w, b, None, out, dims, xs, os_, [0, 0, 0, 0])
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
+    warmup = warm_up(call, args.warmup)
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -182,7 +212,7 @@ def conv3d_bench(args):
     print(json.dumps({
         "metric": "conv3d fwd TFLOP/s (fp16 NDHWC implicit GEMM), 1xMI355X",
         "value": round(flops * args.steps / wall / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup,
+        "steps": args.steps, "warmup": warmup,
         "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
         "dtype": "fp16", "data": "synthetic: x, w ~ 0.25 N(0,1), bias ~ N(0,1), seeded",
         "config": {"workload": "conv3d x[1,512,8,64,64] w[512,512,3,3,3] stride 1, bias"},
@@ -264,9 +294,7 @@ def main():
     attn = gfx906_amd.extension().attn
     flops = gfx906_amd.flops(w["B"], w["H"], w["Sq"], w["Skv"], w["D"])
 
-    for _ in range(args.warmup):
-        attn(q, k, v, scale)
-    torch.cuda.synchronize()
+    warmup = warm_up(lambda: attn(q, k, v, scale), args.warmup)
 
     # Per-launch HIP events on the stream the kernel runs on (the current stream).
     stream = torch.cuda.current_stream()
@@ -300,7 +328,7 @@ def main():
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -49,3 +49,28 @@ def test_profile_figures_match_the_committed_summary():
 def test_conv_profile_traffic_is_read():
     fig = bench.read_profile_figures(bench.CONV_TRAFFIC_FILE)
     assert fig["traffic"] == 217144832 + 23617536
+
+
+def test_warm_up_count(monkeypatch):
+    """An explicit --warmup is run exactly; the default sizes the count to
+    about WARMUP_MS of launches from one timed launch, within its bounds."""
+    import time
+
+    import torch
+
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    calls = []
+
+    def launch(ms):
+        def call():
+            calls.append(1)
+            time.sleep(ms * 1e-3)
+        return call
+
+    assert bench.warm_up(launch(0), 7) == 7 and len(calls) == 7
+    calls.clear()
+    n = bench.warm_up(launch(5), None)  # ~50 launches of 5 ms
+    assert n == len(calls)
+    assert bench.MIN_WARMUP <= n <= bench.WARMUP_MS / 5 + 1
+    calls.clear()
+    assert bench.warm_up(launch(20), None) == bench.MIN_WARMUP == len(calls)
