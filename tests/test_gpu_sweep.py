@@ -24,7 +24,7 @@ from oracle.attention import make_inputs, sdpa_math_fp32, within_tolerance
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-N_CASES = 40
+N_CASES = 100
 HEAD_DIMS = [8, 16, 24, 32, 40, 48, 56, 64, 64, 128, 128, 128, 512, 512]
 
 
