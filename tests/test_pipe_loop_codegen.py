@@ -109,3 +109,33 @@ def test_d128_main_loop_instruction_mix(kernel_asm):
         assert addr <= 2, (name, addr)
         # every LDS read of K and V is one instruction with an immediate offset
         assert c["ds_read_b128"] == 8 * blocks and c["ds_read_b64_tr_b16"] == 16 * blocks, name
+
+
+RESOURCES = re.compile(r"^(_Z\w+):.*?^\.Lfunc_end\d+:.*?; TotalNumVgprs: (\d+)\n; ScratchSize: (\d+)"
+                       r".*?; Occupancy: (\d+)", re.S | re.M)
+# Waves per SIMD each kernel is designed for (its register budget).
+OCCUPANCY = [("attn_fwd_pipeINS_3CfgILi128", 2), ("attn_fwd_pipeINS_3CfgILi64", 4),
+             ("attn_fwd_d512w", 1), ("attn_fwd_d512I", 2), ("attn_fwd_kvres", 4),
+             ("attn_combine", 8)]
+
+
+def test_kernels_do_not_spill(kernel_asm):
+    """A scratch reload in a ring kernel's loop comes with a vmcnt(0) wait, which
+    drains the tile loads in flight: no attention kernel may use scratch, except
+    the K/V-resident kernel's one register kept across its work items (stored
+    once before the item loop, reloaded once per item, outside the block loop)."""
+    seen = set()
+    for m in RESOURCES.finditer(kernel_asm):
+        name, vgprs, scratch, occ = m.group(1), int(m.group(2)), int(m.group(3)), int(m.group(4))
+        want = [o for pat, o in OCCUPANCY if pat in name]
+        if not want:
+            continue
+        seen.add(next(pat for pat, _ in OCCUPANCY if pat in name))
+        assert occ >= want[0] and vgprs <= 512 // want[0], (name, vgprs, occ)
+        if "attn_fwd_kvres" in name:
+            body = functions(kernel_asm, re.escape(name))[name]
+            assert scratch <= 16, (name, scratch)
+            assert sum(l.lstrip().startswith("scratch_") for l in body) <= 2, name
+        else:
+            assert scratch == 0, (name, scratch)
+    assert seen == {pat for pat, _ in OCCUPANCY}, seen
