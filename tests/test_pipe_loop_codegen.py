@@ -139,3 +139,24 @@ def test_kernels_do_not_spill(kernel_asm):
         else:
             assert scratch == 0, (name, scratch)
     assert seen == {pat for pat, _ in OCCUPANCY}, seen
+
+
+@pytest.fixture(scope="module")
+def conv_asm(tmp_path_factory):
+    out = tmp_path_factory.mktemp("asm") / "conv3d_kernel.s"
+    cmd = [build.hipcc(), *build.HIP_FLAGS, "--cuda-device-only", "-S", f"-I{build.INCLUDE}",
+           str(build.CSRC / "conv3d_kernel.hip"), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        pytest.skip(f"hipcc unavailable or failed: {res.stderr[-500:]}")
+    return out.read_text()
+
+
+def test_conv3d_kernels_do_not_spill(conv_asm):
+    """Every conv3d tile configuration keeps two waves per SIMD and no scratch
+    (the small-C 4x32x256 kernel spilled before its k-tile scheduling barrier)."""
+    found = [(m.group(1), int(m.group(2)), int(m.group(3)), int(m.group(4)))
+             for m in RESOURCES.finditer(conv_asm) if "conv3d_mfma" in m.group(1)]
+    assert len(found) == 14, len(found)  # seven configurations, each for small and large C
+    for name, vgprs, scratch, occ in found:
+        assert scratch == 0 and occ >= 2 and vgprs <= 256, (name, vgprs, scratch, occ)
