@@ -40,6 +40,9 @@ CONV_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3d_vae_kernel_trace.txt"
 WARMUP_MS = 250.0  # default warm-up: about this much back-to-back work ...
 MIN_WARMUP = 30  # ... and at least this many launches
 MAX_WARMUP = 20000
+# The reference's D = 512 benchmark (bench_d512.py:21, :63): one VAE mid-block
+# head, B1 H1 D512, q, k, v ~ N(0,1), at these sequence lengths.
+VAE_D512 = {"vae1k": 1024, "vae4k": 4096, "vae9k": 9216, "vae129k": 129600}
 
 
 def parse_args():
@@ -54,13 +57,19 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--torch-sdpa", action="store_true",
+                    help="also time torch's fused scaled_dot_product_attention (flash backend, "
+                         "else memory-efficient) on the same inputs, the same way")
     ap.add_argument("--workload", default="ns",
-                    choices=["ns", "ns_h8", "c1", "c2", "c3", "c4", "c5", "conv3d_vae"],
+                    choices=["ns", "ns_h8", "c1", "c2", "c3", "c4", "c5", *VAE_D512,
+                             "conv3d_vae"],
                     help="BASELINE.json config to run (default: the north star the metric is "
                          "quoted on; others are for profiling: ns_h8 is the north star with 8 "
                          "of its 16 heads, the same kernel and per-workgroup work at half the "
                          "cycles, for counters that would saturate on the full workload; "
-                         "conv3d_vae times the conv3d kernel on a 512->512 3x3x3 VAE layer)")
+                         "vae1k .. vae129k are the reference's D = 512 benchmark shapes, one "
+                         "head of 1024 to 129600 tokens; conv3d_vae times the conv3d kernel on "
+                         "a 512->512 3x3x3 VAE layer)")
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
                     help="attention input type (profiling; the metric is quoted for fp16)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -255,6 +264,40 @@ def cpu_baseline():
     }
 
 
+def torch_sdpa_leg(attn, q, k, v, scale, flops, args):
+    """torch.nn.functional.scaled_dot_product_attention with its flash backend
+    (else the memory-efficient one; never the math path) on the same contiguous
+    inputs, timed like the kernel: warm-up, then args.steps launches with HIP
+    events on the current stream. None when neither backend serves the call."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    ours = attn(q, k, v, scale)
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel(backend):
+                ref = sdpa(q, k, v, scale=scale)
+                torch.cuda.synchronize()
+                warm_up(lambda: sdpa(q, k, v, scale=scale), args.warmup)
+                stream = torch.cuda.current_stream()
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(args.steps)]
+                for a, b in ev:
+                    a.record(stream)
+                    sdpa(q, k, v, scale=scale)
+                    b.record(stream)
+                torch.cuda.synchronize()
+        except RuntimeError:  # backend cannot serve this shape or dtype
+            continue
+        avg = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+        achieved = flops / (avg * 1e-3) / 1e12
+        return {"backend": backend.name, "kernel_ms_avg": round(avg, 4),
+                "achieved": round(achieved, 2), "frac": round(achieved / PEAK_TFLOPS, 4),
+                "max_abs_vs_kernel": (ref.float() - ours.float()).abs().max().item()}
+    return None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -284,6 +327,9 @@ def main():
         w, mults, seed = WORKLOAD, (1.0, 1.0), SEED
     elif args.workload == "ns_h8":
         w, mults, seed = dict(WORKLOAD, H=8), (1.0, 1.0), SEED
+    elif args.workload in VAE_D512:
+        S = VAE_D512[args.workload]
+        w, mults, seed = dict(B=1, H=1, Sq=S, Skv=S, D=512), (1.0, 1.0), SEED
     else:
         B, H, Sq, Skv, D, qm, vm, seed = CONFIGS[args.workload]
         w, mults = dict(B=B, H=H, Sq=Sq, Skv=Skv, D=D), (qm, vm)
@@ -338,6 +384,8 @@ def main():
         "config": {"workload": (f"attn_fwd B{w['B']} H{w['H']} Sq{w['Sq']} Skv{w['Skv']} "
                                 f"D{w['D']} {args.dtype}, scale 1/sqrt(D), no mask ("
                                 + ("BASELINE.json north star" if args.workload == "ns"
+                                   else "the reference's bench_d512.py shape"
+                                   if args.workload in VAE_D512
                                    else f"BASELINE.json config {args.workload}") + ")"), **w,
                    "parallelism": "single GPU"},
         "pct_peak": round(100 * value / PEAK_TFLOPS, 2),
@@ -360,6 +408,8 @@ def main():
                      "source": os.path.relpath(TRAFFIC_FILE, ROOT)
                      if north_star and os.path.isfile(TRAFFIC_FILE) else None},
     }
+    if args.torch_sdpa:
+        result["torch_sdpa"] = torch_sdpa_leg(attn, q, k, v, scale, flops, args)
     if not args.no_cpu and args.workload == "ns" and args.dtype == "fp16":
         result["cpu_baseline"] = cpu_baseline()
     else:

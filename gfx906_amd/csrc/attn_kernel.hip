@@ -1988,9 +1988,23 @@ int cu_count() {
     return n;
 }
 
-// Split of the key range for problems whose grid leaves CUs idle: enough
-// splits to give every workgroup slot (one per CU for D = 128 and 512, two
-// for D <= 64) a workgroup, with at least four key tiles per split.
+// Split of the key range for problems whose grid leaves CUs idle (fewer
+// workgroups than slots: one per CU for D = 128 and 512, two for D <= 64),
+// with at least four key tiles per split. The count minimises an estimate of
+// the run time in tile times of one workgroup: rounds of workgroups over the
+// slots x (tiles per split, rounded up to the kernel's loop step: four tiles
+// for D <= 128, two for D = 512, + kSplitFixedTiles for a workgroup's prologue
+// and epilogue), x kSplitAloneRate when a D <= 64 round leaves every CU one
+// workgroup (its tiles then run faster), plus the HBM traffic of the partial
+// results (fp32 O written by the split kernel and read back by attn_combine)
+// at kSplitTileBytes per tile time. The constants are fitted to interleaved
+// timings on the MI355X. Filling the slots exactly is what matters most: one
+// D = 512 head of 9216 queries (72 query tiles) in 4 splits is 288
+// workgroups, two rounds for 1.125 rounds of work; 3 splits run in one and
+// take 0.187 instead of 0.287 ms.
+constexpr double kSplitFixedTiles = 2.0;
+constexpr double kSplitAloneRate = 0.7;
+constexpr double kSplitTileBytes = 11.0e6;
 struct SplitPlan {
     int nsplit, split_len;
 };
@@ -2002,11 +2016,32 @@ SplitPlan plan_split(int B, int H, int Sq, int Skv, int D) {
     const long long slots = (long long)cu_count() * per_cu;
     if (Skv == 0 || units == 0 || units >= slots) return {1, 0};
     const int tiles = (Skv + bn - 1) / bn;
-    int ns = (int)std::min<long long>((slots + units - 1) / units, tiles / 4);
-    if (ns <= 1) return {1, 0};
-    const int per = (tiles + ns - 1) / ns;  // tiles per split
-    ns = (tiles + per - 1) / per;           // no empty splits
-    return {ns, per * bn};
+    const double partial_bytes = 2.0 * B * H * (double)Sq * D * 4;  // per split
+    const long long cus = cu_count();
+    const int step = D == 512 ? 2 : 4;
+    auto estimate = [&](int ns, int per) {
+        const long long wgs = units * ns, rounds = (wgs + slots - 1) / slots;
+        const double rate = per_cu == 2 && wgs <= cus ? kSplitAloneRate : 1.0;
+        const int run = (per + step - 1) / step * step;
+        return rounds * (run + kSplitFixedTiles) * rate +
+               (ns > 1 ? ns * partial_bytes / kSplitTileBytes : 0.0);
+    };
+    SplitPlan best{1, 0};
+    double best_t = estimate(1, tiles);
+    // The search stops at eight times the count that fills the slots once
+    // (eight rounds of workgroups).
+    const long long fill = (slots + units - 1) / units;
+    const int max_ns = (int)std::min<long long>(tiles / 4, 8 * fill);
+    for (int ns = 2; ns <= max_ns; ++ns) {
+        const int per = (tiles + ns - 1) / ns;  // tiles per split
+        if ((tiles + per - 1) / per != ns) continue;  // would leave a split empty
+        const double t = estimate(ns, per);
+        if (t < best_t) {
+            best_t = t;
+            best = {ns, per * bn};
+        }
+    }
+    return best;
 }
 
 size_t split_ws_bytes(const SplitPlan& p, int B, int H, int Sq, int D) {

@@ -255,6 +255,10 @@ def test_split_workspace_bytes():
     assert lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 512) == 8 * 4096 * (512 + 2) * 4 + 16
     # too few key tiles to split (fewer than 8 = 2 splits x 4 tiles)
     assert lib.attn_split_workspace_bytes(1, 1, 300, 400, 128) == 0
+    # 72 query tiles: 3 splits fill the 256 CUs in one round (4 would take two)
+    assert lib.attn_split_workspace_bytes(1, 1, 9216, 9216, 512) == 3 * 9216 * (512 + 2) * 4 + 16
+    # 200 query tiles: a split would take two rounds of half the work, so none
+    assert lib.attn_split_workspace_bytes(1, 1, 25600, 4096, 512) == 0
     for bad in ((0, 1, 8, 8, 64), (1, 1, 8, 0, 64), (1, 1, 8, 8, 96)):
         assert lib.attn_split_workspace_bytes(*bad) == 0
 
@@ -263,10 +267,11 @@ def test_split_static_scratch_capacity_and_rejection():
     lib = gfx906_amd.capi()
     cap = lib.attn_split_scratch_capacity()
     assert cap == 96 << 20
-    # One D=512 head of 25600 queries splits in two: 2*25600*(512+2)*4 bytes > 96 MiB.
-    need = lib.attn_split_workspace_bytes(1, 1, 25600, 4096, 512)
-    assert need > cap
-    rc = lib.attn_fwd_split_static(P, P, P, P, 1, 1, 25600, 4096, 512, 0.1, None, 0,
+    # One D=512 head of 24576 queries over 65536 keys splits in four (three
+    # rounds of 192 workgroups): 4*24576*(512+2)*4 bytes > 96 MiB.
+    need = lib.attn_split_workspace_bytes(1, 1, 24576, 65536, 512)
+    assert need == 4 * 24576 * (512 + 2) * 4 + 16 > cap
+    rc = lib.attn_fwd_split_static(P, P, P, P, 1, 1, 24576, 65536, 512, 0.1, None, 0,
                                    None, None, None, None)
     assert rc == 1 and b"exceeds the static scratch" in lib.attn_last_error()
     # Within capacity, arguments are validated as for attn_fwd_split.
