@@ -2075,9 +2075,10 @@ SplitPlan plan_split(int B, int H, int Sq, int Skv, int D) {
     SplitPlan best{1, 0};
     double best_t = estimate(1, tiles);
     // The search stops at eight times the count that fills the slots once
-    // (eight rounds of workgroups).
+    // (eight rounds of workgroups), and at 1024 splits (a few microseconds of
+    // host time per call at most).
     const long long fill = (slots + units - 1) / units;
-    const int max_ns = (int)std::min<long long>(tiles / 4, 8 * fill);
+    const int max_ns = (int)std::min<long long>(std::min<long long>(tiles / 4, 8 * fill), 1024);
     for (int ns = 2; ns <= max_ns; ++ns) {
         const int per = (tiles + ns - 1) / ns;  // tiles per split
         if ((tiles + per - 1) / per != ns) continue;  // would leave a split empty
