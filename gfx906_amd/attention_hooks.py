@@ -127,7 +127,7 @@ class DitRouter:
 def _token_view(x):
     """[b, c, h, w] -> [b, 1, h*w, c] view (sequence stride 1, channel stride
     h*w). The op reads and writes such views in place, or copies them where
-    that is faster (h*w > 4096)."""
+    that is faster (h*w > 6400)."""
     b, c, h, w = x.shape
     return x.reshape(b, c, h * w).transpose(1, 2).unsqueeze(1)
 

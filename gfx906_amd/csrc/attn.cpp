@@ -20,12 +20,13 @@
 //    only other layouts are copied, where the reference always calls
 //    .contiguous() (attn.cpp:15). The VAE's token-contiguous views
 //    ([b, c, h*w] seen as [b, 1, h*w, c], deploy/gfx906_attention.py:102-104,
-//    D = 512) are read in place, q and out with them, up to Skv = 4096; past
+//    D = 512) are read in place, q and out with them, up to Skv = 6400; past
 //    that they are copied, on purpose: the in-place kernel needs transposing
 //    LDS reads for K and runs 16 query rows per wave, a cost that grows with
 //    Skv^2 while the copies grow with Skv (measured on MI355X with split key
-//    ranges: in place 0.115 against 0.120 ms copied at h*w = 4096, 0.185
-//    against 0.174 ms at 4608, 0.85 against 0.62 ms at 16384).
+//    ranges, in place against copy and the 32-row kernel: 0.115 against 0.127
+//    ms at h*w = 4608, 0.161 against 0.169 ms at 6400, 0.226 against 0.192 ms
+//    at 7056, 0.775 against 0.605 ms at 16384).
 //  * `out`, if given, is written instead of allocating: any [B, H, Sq, D]
 //    view of q's dtype and device whose elements do not overlap, e.g. the
 //    transpose of a [B, Sq, H, D] buffer or the VAE's [b, 1, h*w, c] view of
@@ -81,7 +82,7 @@ bool token_contiguous_kv(const torch::Tensor& t) {
 
 // Largest Skv for which reading token-contiguous k/v in place beats copying
 // them (see the file comment).
-constexpr int64_t kInPlaceMaxSkv = 4096;
+constexpr int64_t kInPlaceMaxSkv = 6400;
 
 torch::Tensor as_input(const torch::Tensor& t, bool kv) {
     return readable_in_place(t, kv) ? t : t.clone(at::MemoryFormat::Contiguous);

@@ -275,10 +275,10 @@ def test_token_contiguous_d512_in_place_via_capi(dtype, b, h, w):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("h,w", [(12, 20), (96, 96)])
+@pytest.mark.parametrize("h,w", [(12, 20), (72, 72), (96, 96)])
 def test_op_vae_views_and_nchw_out(dtype, h, w):
     # The torch op on the VAE's views, written through a [b, c, h, w] view:
-    # read in place up to 4096 tokens (no allocation beyond the split
+    # read in place up to 6400 tokens (no allocation beyond the split
     # workspace), copied above.
     g = torch.Generator().manual_seed(3)
     xs = [(torch.randn(1, 512, h, w, generator=g) * 0.5).to(dtype).to(DEV) for _ in range(3)]
@@ -293,7 +293,7 @@ def test_op_vae_views_and_nchw_out(dtype, h, w):
     ws = gfx906_amd.capi().attn_split_workspace_bytes(1, 1, h * w, h * w, 512)
     copies = 4 * h * w * 512 * 2
     extra = torch.cuda.max_memory_allocated() - base
-    if h * w <= 4096:  # only the split workspace (allocator blocks of 512 bytes)
+    if h * w <= 6400:  # only the split workspace (allocator blocks of 512 bytes)
         assert extra <= (ws + 511) // 512 * 512, (extra, ws)
     else:
         assert extra >= copies, (extra, copies)
