@@ -259,6 +259,12 @@ def test_split_workspace_bytes():
     assert lib.attn_split_workspace_bytes(1, 1, 9216, 9216, 512) == 3 * 9216 * (512 + 2) * 4 + 16
     # 200 query tiles: a split would take two rounds of half the work, so none
     assert lib.attn_split_workspace_bytes(1, 1, 25600, 4096, 512) == 0
+    # D = 128, 64 key tiles: 16 splits of 4 tiles; 11 or 13 would leave 6 or 5
+    # tiles per split, which the kernel's groups of four tiles run as 8
+    assert lib.attn_split_workspace_bytes(1, 1, 4096, 4096, 128) == 16 * 4096 * (128 + 2) * 4 + 16
+    # D = 64 runs two workgroups per CU: 4 splits (256 workgroups, one per CU)
+    # beat 8 (512, two per CU) on 8 heads of 2048 queries
+    assert lib.attn_split_workspace_bytes(1, 8, 2048, 2048, 64) == 4 * 8 * 2048 * (64 + 2) * 4 + 16
     for bad in ((0, 1, 8, 8, 64), (1, 1, 8, 0, 64), (1, 1, 8, 8, 96)):
         assert lib.attn_split_workspace_bytes(*bad) == 0
 
