@@ -133,6 +133,34 @@ def test_capi_bshd_layout_bit_exact(dtype, D):
     assert torch.equal(o, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D,Skv", [(64, 201), (128, 201), (512, 201), (512, 4100)])
+def test_capi_output_rows_not_16_byte_aligned(dtype, D, Skv):
+    # Output rows D + 4 elements apart (8-byte aligned, not 16): the kernels
+    # store such rows directly instead of staging whole rows through LDS; the
+    # result must equal the contiguous output bit for bit (Skv = 4100 at
+    # D = 512 also takes the split key range path).
+    q, k, v = (t.to(dtype).to(DEV) for t in make_inputs(1, 3, 150, Skv, D, seed=D + 45))
+    code = ATTN_DTYPE_BF16 if dtype == torch.bfloat16 else ATTN_DTYPE_F16
+    lib = gfx906_amd.capi()
+    need = lib.attn_split_workspace_bytes(1, 3, 150, Skv, D)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    padded = torch.full((1, 3, 150, D + 4), float("nan"), dtype=dtype, device=DEV)
+    outs = []
+    for o in (torch.empty_like(q), padded[..., :D]):
+        st = lambda t: (ctypes.c_longlong * 4)(*[t.stride(i) for i in range(4)])
+        rc = lib.attn_fwd_split(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), 1, 3, 150,
+                                Skv, D, D ** -0.5, stream, code, None, None, None, st(o),
+                                ctypes.c_void_p(ws.data_ptr()), need)
+        assert rc == 0, lib.attn_last_error()
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert (need > 0) == (Skv == 4100)
+    assert torch.equal(outs[1], outs[0])
+    assert torch.isnan(padded[..., D:]).all()  # the padding is untouched
+
+
 def test_capi_broadcast_kv_over_heads():
     # k/v of one head shared by all heads: head stride 0.
     q, k, v = (t.to(DEV) for t in make_inputs(2, 4, 96, 150, 128, seed=41))
