@@ -21,6 +21,7 @@ MATH in fp32 on the CPU. Each case prints its parameters first.
 """
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -31,7 +32,8 @@ from oracle.attention import make_inputs, sdpa_math_fp32, within_tolerance
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 48
+# GFX906_AMD_CAPI_SWEEP_CASES=400 runs a longer sweep (same generator, more seeds).
+N_CASES = int(os.environ.get("GFX906_AMD_CAPI_SWEEP_CASES", "48"))
 HEAD_DIMS = [8, 24, 40, 56, 64, 64, 128, 128, 128, 512, 512]
 F16, BF16 = 0, 1
 
