@@ -2054,7 +2054,11 @@ constexpr double kSplitTileBytes = 11.0e6;
 struct SplitPlan {
     int nsplit, split_len;
 };
-SplitPlan plan_split(int B, int H, int Sq, int Skv, int D) {
+size_t split_ws_bytes(const SplitPlan& p, int B, int H, int Sq, int D);
+// ws_cap bounds the workspace of the chosen plan (the static scratch's size
+// for callers that pass none); counts whose partial results do not fit are
+// skipped, down to no split at all.
+SplitPlan plan_split(int B, int H, int Sq, int Skv, int D, size_t ws_cap = (size_t)-1) {
     const int bm = D == 512 ? Cfg512::BM : (D == 128 ? Cfg128::BM : Cfg64::BM);
     const int bn = D == 512 ? Cfg512::BN : Cfg128::BN;
     const int per_cu = D == 512 || D == 128 ? 1 : 2;
@@ -2082,6 +2086,7 @@ SplitPlan plan_split(int B, int H, int Sq, int Skv, int D) {
     for (int ns = 2; ns <= max_ns; ++ns) {
         const int per = (tiles + ns - 1) / ns;  // tiles per split
         if ((tiles + per - 1) / per != ns) continue;  // would leave a split empty
+        if (split_ws_bytes({ns, per * bn}, B, H, Sq, D) > ws_cap) break;  // grows with ns
         const double t = estimate(ns, per);
         if (t < best_t) {
             best_t = t;
@@ -2200,61 +2205,94 @@ extern "C" const char* attn_last_error(void) { return g_err[0] ? g_err : nullptr
 
 namespace {
 
-// Workspace of attn_fwd_split_static: the split-key partial results live in
-// this file-scope device array instead of caller memory. Each GPU the
-// library runs on holds its own copy (from the first use until the process
-// ends). Host code must not pass `scratch` itself to a kernel (on the host it
-// names a stand-in, not device memory): it uses the device address that
-// hipGetSymbolAddress returns, looked up once per device. The kernels write
-// every workspace entry the merge reads within the same call, so nothing is
-// cleared between calls; calls that overlap on one GPU share the array and
-// race.
+// Workspace of the calls that split without a caller workspace
+// (attn_fwd_split_static, and launch() / attn_fwd() for grids too small for
+// the GPU): the split-key partial results live in this file-scope device
+// array. It is part of the library's code object, so every GPU on which any
+// kernel of the library is loaded holds its own copy (kScratchBytes) until
+// the process ends, whether or not a call ever uses it. Host code must not
+// pass `scratch` itself to a kernel (on the host it names a stand-in, not
+// device memory): it uses the device address that hipGetSymbolAddress
+// returns, looked up once per device. The kernels write every workspace
+// entry the merge reads within the same call, so nothing is cleared between
+// calls.
+//
+// Calls that use the array are ordered on the GPU, whatever streams they are
+// issued on: each records `done` on its stream after its kernels, and a call
+// on another stream first makes its stream wait for that event (the host
+// lock keeps wait, launches and record of one call together, so the calls
+// form one chain per device). A call made under stream capture neither
+// waits nor records (an event recorded outside the graph cannot order its
+// replays): a graph that contains one is ordered only by the stream it is
+// launched on, and must not run concurrently with other calls that use the
+// array on that device.
 constexpr size_t kScratchBytes = size_t(96) << 20;
 static __device__ __align__(256) char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
+struct DevScratch {
+    void* ptr;           // device address of `scratch`
+    hipEvent_t done;     // recorded after the last call outside capture that used it
+    hipStream_t last;    // the stream of that call
+    bool recorded;
+};
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices];
+DevScratch g_scratch[kMaxDevices];
 
-// This device's address of `scratch`, for the device `stream` belongs to (the
-// current device for the null stream). Returns 0, or an attn_fwd status with
+// Device of `stream` (the current device for the null stream), or -1 with
 // the error message set.
-int device_scratch(hipStream_t stream, void** out) {
-    int dev = 0, cur = 0;
-    hipError_t e = hipGetDevice(&cur);
-    if (e == hipSuccess) {
-        dev = cur;
-        if (stream) e = hipStreamGetDevice(stream, &dev);
+int stream_device(hipStream_t stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && stream) e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) {
+        set_err(hipGetErrorString(e));
+        return -1;
     }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_err("attn: device index beyond the scratch table");
+        return -1;
+    }
+    return dev;
+}
+
+// Looks up `scratch` on device dev and creates its ordering event, once.
+// Caller holds g_scratch_mu. Returns 0, or 2 with the error message set.
+int scratch_setup(int dev) {
+    DevScratch& d = g_scratch[dev];
+    if (d.ptr) return 0;
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && dev != cur) e = hipSetDevice(dev);
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;
     }
-    if (dev < 0 || dev >= kMaxDevices) return fail("attn: device index beyond the scratch table");
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
-            set_err(hipGetErrorString(e));
-            return 2;
-        }
-        void* p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (dev != cur) {
-            const hipError_t r = hipSetDevice(cur);
-            if (e == hipSuccess) e = r;
-        }
-        if (e != hipSuccess || !p) {
-            set_err(e != hipSuccess ? hipGetErrorString(e) : "attn: no device address for scratch");
-            return 2;
-        }
-        g_scratch_ptr[dev] = p;
+    void* p = nullptr;
+    hipEvent_t ev = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && !p) e = hipErrorInvalidSymbol;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (dev != cur) {
+        const hipError_t r = hipSetDevice(cur);
+        if (e == hipSuccess) e = r;
     }
-    *out = g_scratch_ptr[dev];
+    if (e != hipSuccess) {
+        if (ev) (void)hipEventDestroy(ev);
+        set_err(hipGetErrorString(e));
+        return 2;
+    }
+    d.ptr = p;
+    d.done = ev;
+    d.last = nullptr;
+    d.recorded = false;
     return 0;
 }
 
 // attn_fwd_ex (workspace_bytes == SIZE_MAX: never split), attn_fwd_split
-// and, with use_scratch, attn_fwd_split_static (workspace: the static scratch).
+// (caller workspace) and, with use_scratch, attn_fwd_split_static, launch()
+// and attn_fwd() (workspace: the static scratch, split plans bounded by its
+// size).
 int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, int H, int Sq,
                   int Skv, int D, float scale, hipStream_t stream, int dtype,
                   const long long* q_strides, const long long* k_strides,
@@ -2295,34 +2333,62 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     a.ws_ml = nullptr;
     a.o16 = (uintptr_t)o % 16 == 0 && so.b % 8 == 0 && so.h % 8 == 0 && so.s % 8 == 0 && so.d == 1;
     a.q_lds = sq.s <= (1LL << 24) && Skv > 1024;
-    if (workspace_bytes != (size_t)-1) {  // attn_fwd_split: split the keys if it pays
-        const SplitPlan p = plan_split(B, H, Sq, Skv, D);
-        const size_t need = split_ws_bytes(p, B, H, Sq, D);
-        if (need && use_scratch) {
-            if (need > kScratchBytes) {
-                set_err("attn: this problem's split workspace exceeds the static scratch "
-                        "(attn_split_scratch_capacity()); use attn_fwd_split with a workspace");
-                return 1;
-            }
-            const int rc = device_scratch(stream, &workspace);
+    SplitPlan p{1, 0};
+    if (workspace_bytes != (size_t)-1)  // split the keys if it pays
+        p = plan_split(B, H, Sq, Skv, D, use_scratch ? kScratchBytes : (size_t)-1);
+    const size_t need = split_ws_bytes(p, B, H, Sq, D);
+    DevScratch* ds = nullptr;
+    std::unique_lock<std::mutex> lock(g_scratch_mu, std::defer_lock);
+    bool capturing = false;
+    if (need && use_scratch) {
+        const int dev = stream_device(stream);
+        if (dev < 0) return 2;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(stream, &st);
+        if (e != hipSuccess) {
+            set_err(hipGetErrorString(e));
+            return 2;
+        }
+        capturing = st != hipStreamCaptureStatusNone;
+        lock.lock();
+        ds = &g_scratch[dev];
+        if (!ds->ptr) {
+            if (capturing)
+                return fail("attn: the static scratch of this device is set up by the first call "
+                            "that splits outside stream capture; make one such call before "
+                            "capturing");
+            const int rc = scratch_setup(dev);
             if (rc) return rc;
-            workspace_bytes = kScratchBytes;
         }
-        if (need) {
-            if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16) {
-                set_err("attn: workspace missing, misaligned or smaller than "
-                        "attn_split_workspace_bytes()");
-                return 1;
-            }
-            a.nsplit = p.nsplit;
-            a.split_len = p.split_len;
-            a.ws_o = (float*)workspace;
-            a.ws_ml = a.ws_o + (size_t)p.nsplit * B * H * Sq * D;
+        if (!capturing && ds->recorded && ds->last != stream &&
+            (e = hipStreamWaitEvent(stream, ds->done, 0)) != hipSuccess) {
+            set_err(hipGetErrorString(e));
+            return 2;
         }
+        workspace = ds->ptr;
+        workspace_bytes = kScratchBytes;
+    }
+    if (need) {
+        if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16) {
+            set_err("attn: workspace missing, misaligned or smaller than "
+                    "attn_split_workspace_bytes()");
+            return 1;
+        }
+        a.nsplit = p.nsplit;
+        a.split_len = p.split_len;
+        a.ws_o = (float*)workspace;
+        a.ws_ml = a.ws_o + (size_t)p.nsplit * B * H * Sq * D;
     }
     const bool tl = token_contiguous(sk, sv, D);
-    const hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, tl, stream)
-                                                  : launch_t<f16>(a, tl, stream);
+    hipError_t e = dtype == ATTN_DTYPE_BF16 ? launch_t<bf16>(a, tl, stream)
+                                            : launch_t<f16>(a, tl, stream);
+    if (e == hipSuccess && ds && !capturing) {
+        e = hipEventRecord(ds->done, stream);
+        if (e == hipSuccess) {
+            ds->last = stream;
+            ds->recorded = true;
+        }
+    }
     if (e != hipSuccess) {
         set_err(hipGetErrorString(e));
         return 2;
@@ -2370,8 +2436,8 @@ extern "C" int attn_fwd_split_static(const void* q, const void* k, const void* v
 
 extern "C" int attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,
                         int Sq, int Skv, int D, float scale, hipStream_t s) {
-    return attn_fwd_ex(q, k, v, o, B, H, Sq, Skv, D, scale, s, ATTN_DTYPE_F16, nullptr, nullptr,
-                       nullptr, nullptr);
+    return attn_fwd_impl(q, k, v, o, B, H, Sq, Skv, D, scale, s, ATTN_DTYPE_F16, nullptr, nullptr,
+                         nullptr, nullptr, nullptr, 0, true);
 }
 
 extern "C" void launch(const void* q, const void* k, const void* v, void* o, int B, int H,

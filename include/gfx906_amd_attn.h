@@ -8,7 +8,15 @@
  * D must be <= 64 and a multiple of 8, or 128, or 512. Sq != Skv is allowed.
  * o[b,h,i,:] = sum_j softmax_j(scale * <q[b,h,i,:], k[b,h,j,:]>) v[b,h,j,:],
  * rounded to the element type; rows with Skv == 0 are written as zeros.
- * Calls are asynchronous on `stream` and keep no state between calls.
+ * Calls are asynchronous on `stream`. The only state kept between calls is
+ * the static scratch of the calls that split key ranges without a caller
+ * workspace (launch(), attn_fwd(), attn_fwd_split_static()): a device array
+ * of attn_split_scratch_capacity() bytes that is part of the library's code
+ * object, so it is held on every GPU where the library's kernels are loaded,
+ * until the process ends. Those calls are ordered on the GPU across streams
+ * (each waits for the previous one on its device) except under stream
+ * capture, where a captured call neither waits nor is waited for: a graph
+ * that contains one is ordered only by the stream it is launched on.
  */
 #ifndef GFX906_AMD_ATTN_H
 #define GFX906_AMD_ATTN_H
@@ -27,7 +35,9 @@ extern "C" {
 /* Drop-in for the reference entry point of the same name and signature:
  * declared at attn.cpp:4-5, defined at attn_kernel.hip:710-742. Returns
  * nothing; on a rejected argument or launch failure no kernel runs and the
- * reason is available from attn_last_error(). */
+ * reason is available from attn_last_error(). When B*H*Sq is too small to
+ * fill the GPU (a one-head VAE attention) it splits the key range as
+ * attn_fwd_split_static() does, in the static scratch. */
 void launch(const void* q, const void* k, const void* v, void* o,
             int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream);
 
@@ -39,7 +49,8 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o,
              int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream);
 
 /* attn_fwd() for fp16 or bf16 (dtype = ATTN_DTYPE_F16 / ATTN_DTYPE_BF16,
- * the same type for q, k, v and o) and strided tensors. Each *_strides
+ * the same type for q, k, v and o) and strided tensors, never splitting the
+ * key range (one workgroup per batch, head and query tile). Each *_strides
  * points to four element strides {batch, head, sequence, head dim} of that
  * tensor, or is NULL for the contiguous layout. Strides are non-negative;
  * input strides may be 0 (a tensor broadcast over batch or heads) but no two
@@ -82,16 +93,20 @@ int attn_fwd_split(const void* q, const void* k, const void* v, void* o,
                    const long long* v_strides, const long long* o_strides,
                    void* workspace, size_t workspace_bytes);
 
-/* attn_fwd_split() that allocates nothing: the split partial results go to a
- * static device array of the library, attn_split_scratch_capacity() bytes
- * (96 MiB) on each GPU it runs on, held until the process ends. For callers
- * that cannot allocate device memory: code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc. Problems whose split
- * workspace (attn_split_workspace_bytes()) exceeds the capacity are rejected
- * with status 1 before anything runs; problems that do not split use no
- * scratch. Calls that overlap on one GPU share the array and must not run
- * concurrently. Same arguments, results and return codes as attn_fwd_split()
- * otherwise. No counterpart in the reference. */
+/* attn_fwd_split() that allocates nothing: the split partial results go to
+ * the library's static scratch (attn_split_scratch_capacity() bytes, 96 MiB,
+ * on every GPU where the library's kernels are loaded, held until the
+ * process ends). For callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The split count is the best one whose partial results fit the scratch:
+ * the same as attn_fwd_split()'s whenever attn_split_workspace_bytes() <=
+ * capacity (then the results are bit-identical), fewer splits or none
+ * otherwise. Problems that do not split use no scratch. Calls that use the
+ * scratch are ordered across streams on one device (see the top of this
+ * file); under stream capture the first such call on a device must have
+ * been made outside capture (it sets the scratch up), else status 1. Same
+ * arguments and return codes as attn_fwd_split() otherwise. No counterpart
+ * in the reference. */
 int attn_fwd_split_static(const void* q, const void* k, const void* v, void* o,
                           int B, int H, int Sq, int Skv, int D, float scale, hipStream_t stream,
                           int dtype, const long long* q_strides, const long long* k_strides,
