@@ -15,7 +15,10 @@ resident in HBM. Prints one JSON line with the driver's fields plus:
 * ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine)
   over the whole workload, chunked by head and 2048 query rows.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+* ``configs``: kernel rates of BASELINE.json's configs c2-c5, each timed the
+  same way after the north star's timed region (not part of it).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
 """
 
 from __future__ import annotations
@@ -57,6 +60,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip timing the other BASELINE configs after the north star")
     ap.add_argument("--torch-sdpa", action="store_true",
                     help="also time torch's fused scaled_dot_product_attention (flash backend, "
                          "else memory-efficient) on the same inputs, the same way")
@@ -298,6 +303,53 @@ def torch_sdpa_leg(attn, q, k, v, scale, flops, args):
     return None
 
 
+def time_kernel(call, steps):
+    """Per-launch HIP events on the current stream over `steps` back-to-back
+    launches: (average ms, min ms)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for a, b in ev:
+        a.record(stream)
+        call()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return sum(ms) / len(ms), min(ms)
+
+
+CONFIG_LEGS = ("c2", "c3", "c4", "c5")
+
+
+def other_configs(attn, steps):
+    """Kernel rates of BASELINE.json configs c2-c5, measured in this run after
+    the north star's timed region (outside it): seeded fp16 inputs (the
+    oracle's generator, as the parity tests use), then for each config about
+    WARMUP_MS of untimed launches (the card lowers its clock while the inputs
+    are generated on the host) and `steps` launches timed with HIP events."""
+    import gfx906_amd
+    from oracle.attention import CONFIGS, make_inputs
+
+    out = {}
+    for name in CONFIG_LEGS:
+        B, H, Sq, Skv, D, qm, vm, seed = CONFIGS[name]
+        q, k, v = (t.to("cuda") for t in make_inputs(B, H, Sq, Skv, D, qm, vm, seed=seed))
+        scale = D ** -0.5
+        flops = gfx906_amd.flops(B, H, Sq, Skv, D)
+        warmup = warm_up(lambda: attn(q, k, v, scale), None)
+        avg, best = time_kernel(lambda: attn(q, k, v, scale), steps)
+        achieved = flops / (avg * 1e-3) / 1e12
+        out[name] = {"shape": f"B{B} H{H} Sq{Sq} Skv{Skv} D{D}", "kernel_ms_avg": round(avg, 4),
+                     "kernel_ms_min": round(best, 4), "achieved": round(achieved, 2),
+                     "frac": round(achieved / PEAK_TFLOPS, 4), "warmup": warmup, "steps": steps}
+        del q, k, v
+    out["measured"] = ("in this run, after the north star's timed region; TFLOP/s from the "
+                       "average kernel time (HIP events), 4*B*H*Sq*Skv*D FLOP per launch")
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -410,6 +462,9 @@ def main():
     }
     if args.torch_sdpa:
         result["torch_sdpa"] = torch_sdpa_leg(attn, q, k, v, scale, flops, args)
+    if args.workload == "ns" and args.dtype == "fp16" and not args.no_configs:
+        del q, k, v
+        result["configs"] = other_configs(attn, args.steps)
     if not args.no_cpu and args.workload == "ns" and args.dtype == "fp16":
         result["cpu_baseline"] = cpu_baseline()
     else:

@@ -1,6 +1,6 @@
 """In-tree build of the gfx950 attention libraries.
 
-Two shared objects are produced under ``gfx906_amd/lib/``:
+Two shared objects and one program are produced under ``gfx906_amd/lib/``:
 
 * ``libgfx906_amd_attn.so`` -- the HIP kernels and the C ABIs declared in
   ``include/gfx906_amd_attn.h`` and ``include/gfx906_amd_conv3d.h``, compiled
@@ -14,6 +14,9 @@ Two shared objects are produced under ``gfx906_amd/lib/``:
   ``extra_ldflags``. The build directory is ``gfx906_amd/lib`` itself, so the
   module sits next to the kernel library and finds it through an ``$ORIGIN``
   run path.
+* ``launch_harness`` -- a torch-free C++ program that calls ``launch()``
+  through the C ABI on device buffers it allocates itself, as the
+  reference's ``micro3.hip`` does (micro3.hip:4-17).
 
 :func:`build_all` rebuilds both every time it is called. :func:`ensure_kernel_lib`
 is the build-once path the loader uses: rebuild a missing or stale library,
@@ -57,6 +60,10 @@ HIP_FLAGS = [
 ]
 
 KERNEL_SOURCES = [CSRC / "attn_kernel.hip", CSRC / "conv3d_kernel.hip"]
+# A torch-free C caller of launch() (the reference's micro3.hip pattern),
+# linked against the kernel library.
+HARNESS_SOURCE = CSRC / "launch_harness.cpp"
+HARNESS = LIB / "launch_harness"
 BINDING_SOURCES = [CSRC / "attn.cpp", CSRC / "conv3d.cpp", CSRC / "module.cpp"]
 # The binding is host C++ only; HIP types come from the runtime headers.
 EXT_CFLAGS = ["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1"]
@@ -115,9 +122,21 @@ def build_extension() -> Path:
     return EXT_LIB
 
 
+def build_harness() -> Path:
+    """Compile the C caller of launch() against the kernel library (host code
+    only; the library is found through an $ORIGIN run path)."""
+    LIB.mkdir(exist_ok=True)
+    tmp = HARNESS.with_suffix(".tmp")
+    _run([hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", str(HARNESS_SOURCE), "-o", str(tmp),
+          f"-L{LIB}", "-lgfx906_amd_attn", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, HARNESS)
+    return HARNESS
+
+
 def build_all() -> None:
     build_kernel_lib()
     build_extension()
+    build_harness()
 
 
 # -- build once, for the loader -----------------------------------------------------------

@@ -295,3 +295,18 @@ def test_split_rejects_missing_or_short_workspace():
         rc = lib.attn_fwd_split(P, P, P, P, 1, 1, 4096, 4096, 512, 0.04, None, 0,
                                 None, None, None, None, ws, nbytes)
         assert rc == 1 and b"workspace" in lib.attn_last_error()
+
+
+def test_c_harness_links_the_library_and_checks_usage(tmp_path):
+    # The torch-free caller of launch() (gfx906_amd/csrc/launch_harness.cpp)
+    # is built with the library and resolves it from its own directory; bad
+    # usage and missing inputs fail before any HIP call.
+    from gfx906_amd.build import HARNESS
+
+    assert HARNESS.is_file()
+    deps = subprocess.run(["ldd", str(HARNESS)], capture_output=True, text=True).stdout
+    assert str(loader.KERNEL_LIB) in deps
+    assert subprocess.run([str(HARNESS)], capture_output=True).returncode == 1
+    res = subprocess.run([str(HARNESS), str(tmp_path), "1", "1", "4", "4", "64", "0.1", "1"],
+                         capture_output=True, text=True)
+    assert res.returncode == 1 and "cannot read" in res.stderr
