@@ -259,6 +259,16 @@ __device__ __forceinline__ typename Elem<T>::x8 lds_read_tr2(const char* base, i
     return __builtin_bit_cast(typename Elem<T>::x8, u32x4{l[0], l[1], h[0], h[1]});
 }
 
+// The lane's index in its wave, computed where it is used: a volatile asm,
+// which the compiler can neither hoist out of a loop nor share between uses,
+// so nothing holds the value in a register in between (the D <= 64 kernels
+// run at their 128-VGPR limit and spilled such values around the main loop).
+__device__ __forceinline__ int lane_id_here() {
+    int x;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(x));
+    return x;
+}
+
 // Sum / max over lanes i, i+16, i+32, i+48.
 __device__ __forceinline__ float quad_group_sum(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -456,7 +466,7 @@ __device__ __forceinline__ void block_exp(const f32x4& S0, const f32x4& S1,
 // one head adjacent (the splits of one query tile adjacent); block: NW*64
 // threads. The second launch bound is HIP's minimum waves per SIMD
 // (amdgpu_waves_per_eu): OCC workgroups of NW waves over the CU's four SIMDs.
-template <class C, bool PAD, class T, bool SPLIT>
+template <class C, bool PAD, class T, bool SPLIT, bool TILEMAX>
 __global__ void __launch_bounds__(C::NT, C::OCC * C::NW / 4)
 attn_fwd_pipe(const KArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -533,6 +543,12 @@ attn_fwd_pipe(const KArgs a) {
     // of the block's matrix work, +6 % c5 and +1 % c3 with the exact running
     // max below, whose rescales add VALU work).
     constexpr bool kLazy = DP == 128;
+    // D <= 64 with TILEMAX: the running max is raised once per 64-key tile,
+    // over both its blocks, before the first block's P (short key ranges,
+    // where the max rises on most blocks: c3 +7 %, c1 +3 %); without it, once
+    // per 32-key block (long key ranges, where it rarely rises and the tile
+    // max's wait for the second block's scores costs more: c5 -2 %).
+    constexpr bool kTileMax = !kLazy && TILEMAX;
     // Running max of each query column block. D = 128 keeps a lazy one, in
     // log2 units (s*c), raised only when some p exceeds 2^15 (rare after the
     // first blocks: every p stays finite in fp16); it starts at -1e30
@@ -649,15 +665,30 @@ attn_fwd_pipe(const KArgs a) {
         };
         // Scores of keys >= Skv (block keys key0..key0+31) to -inf, for the
         // last one or two blocks only.
+        // (D <= 64 recomputes the lane's key offset here, see lane_id_here;
+        // D = 128 keeps its register, which its code layout is tuned around.)
         auto mask = [&](f32x4 (&S)[2][2], int key0) __attribute__((always_inline)) {
-            if (key0 + 32 > Skv) {
+            if constexpr (DP <= 64) {
+                if (key0 + 32 > Skv) {
+                    const int gm = lane_id_here() >> 4;
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int nb = 0; nb < 2; ++nb)
+                        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
+                            for (int r = 0; r < 4; ++r)
+                                if (key0 + 16 * kb + 4 * gm + r >= Skv) S[kb][nb][r] = -INFINITY;
+                }
+            } else {
+                if (key0 + 32 > Skv) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
+                }
             }
         };
         // O, l and m of column block nb move to the running max m_new
@@ -674,6 +705,16 @@ attn_fwd_pipe(const KArgs a) {
             const float mx = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
             const float my = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
             return max2(max3(mx, S[1][nb][2], S[1][nb][3]), my);
+        };
+        // The lane's largest score over a whole 64-key tile (blocks S and S2).
+        auto lane_max2 = [&](const f32x4 (&S)[2][2], const f32x4 (&S2)[2][2], int nb)
+            __attribute__((always_inline)) {
+            const float a0 = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
+            const float a1 = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
+            const float a2 = max3(S[1][nb][2], S[1][nb][3], S2[0][nb][0]);
+            const float a3 = max3(S2[0][nb][1], S2[0][nb][2], S2[0][nb][3]);
+            const float a4 = max3(S2[1][nb][0], S2[1][nb][1], S2[1][nb][2]);
+            return max2(max3(a0, a1, a2), max3(a3, a4, S2[1][nb][3]));
         };
         // P of one 32-key block. Any rescale of O comes after the PV MFMAs
         // issued before this call.
@@ -720,6 +761,26 @@ attn_fwd_pipe(const KArgs a) {
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
         };
+        // D <= 64 with TILEMAX: P of a tile's two blocks. The first call (S2,
+        // the tile's second block, non-null) raises the running max to the
+        // max over both blocks, then computes S's P; the second (S2 null)
+        // computes the second block's P with no test.
+        auto softmax_tile = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2])
+            __attribute__((always_inline)) {
+            float lp[2];  // unused: the row sums come from the MFMAs below
+            if (S2) {
+                const float lm[2] = {lane_max2(S, *S2, 0), lane_max2(S, *S2, 1)};
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    if (__any(lm[nb] > m_run[nb]))
+                        rescale(nb, max2(m_run[nb], quad_group_max(lm[nb])));
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+                block_exp<T, false>(S[0][nb], S[1][nb], P[nb], -m_run[nb] * c, c, lp[nb]);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) lacc[nb] = E::mma16(aone, P[nb], lacc[nb]);
+        };
 
         f32x4 Sa[2][2], Sb[2][2];
         x8 Pa[2], Pb[2];
@@ -734,14 +795,22 @@ attn_fwd_pipe(const KArgs a) {
             mask(Sa, w * C::BN);
             pv(vp, 1, Pb);     // block 2w-1
             qk(kc, 1, Sb);     // block 2w+1
-            softmax(Sa, Pa);   // block 2w
+            if constexpr (kTileMax) {
+                mask(Sb, w * C::BN + 32);
+                softmax_tile(Sa, Pa, &Sb);  // block 2w, max over blocks 2w and 2w+1
+            } else {
+                softmax(Sa, Pa);            // block 2w
+            }
             __builtin_amdgcn_s_waitcnt(kWaitNext);  // own loads of tile w+1 done
             lds_barrier();                          // every wave's; tile w-1 consumed
             issue(w + 3, kf, vf);
-            mask(Sb, w * C::BN + 32);
+            if constexpr (!kTileMax) mask(Sb, w * C::BN + 32);
             pv(vc, 0, Pa);     // block 2w
             qk(kn, 0, Sa);     // block 2w+2
-            softmax(Sb, Pb);   // block 2w+1
+            if constexpr (kTileMax)
+                softmax_tile(Sb, Pb, nullptr);  // block 2w+1
+            else
+                softmax(Sb, Pb);                // block 2w+1
         };
 
         // Prologue: tiles 0 and 1 in flight, stage 3's V zeroed for the PV of
@@ -806,21 +875,31 @@ attn_fwd_pipe(const KArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
     }
 
+    // Lane indices of the epilogue. D <= 64 runs at 128 VGPRs, and values
+    // kept from the prologue would hold registers across the main loop (two
+    // were spilled around it): they are recomputed from the lane id.
+    int lane_e = lane, ie = i, ge = g, qrow0e = qrow0;
+    if constexpr (DP <= 64) {
+        lane_e = lane_id_here();
+        ie = lane_e & 15;
+        ge = lane_e >> 4;
+        qrow0e = qt * C::BM + wave * 32 + ie;
+    }
     if constexpr (SPLIT) {  // unnormalised O and (m, l) of this key range
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int row = qrow0 + 16 * nb;
+            const int row = qrow0e + 16 * nb;
             const float l = quad_group_sum(lacc[nb][0]);
             if (row < Sq) {
                 const long long r = ((long long)split * a.BH + bh) * Sq + row;
                 float* wo = a.ws_o + r * D;
 #pragma unroll
                 for (int ob = 0; ob < NOB; ++ob) {
-                    const int d0 = 16 * ob + 4 * g;
+                    const int d0 = 16 * ob + 4 * ge;
                     if (!PAD || d0 < D) *reinterpret_cast<f32x4*>(wo + d0) = oacc[ob][nb];
                 }
                 const float m = kLazy ? m_run[nb] : m_run[nb] * c;  // log2 units
-                if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m, l};
+                if (ge == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * r) = f32x2{m, l};
             }
         }
         return;
@@ -842,18 +921,18 @@ attn_fwd_pipe(const KArgs a) {
             const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) {
-                const int d0 = 16 * ob + 4 * g;
+                const int d0 = 16 * ob + 4 * ge;
                 const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
                 const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
                 *reinterpret_cast<LDS_AS typename E::x4*>(
-                    (LDS_AS char*)stg + (16 * nb + i) * RS + d0 * 2) =
+                    (LDS_AS char*)stg + (16 * nb + ie) * RS + d0 * 2) =
                     typename E::x4{h0[0], h0[1], h1[0], h1[1]};
             }
         }
-        const int row0 = qrow0 - i;  // this wave's first row
+        const int row0 = qrow0e - ie;  // this wave's first row
 #pragma unroll
         for (int j = 0; j < 32 * CPR / 64; ++j) {
-            const int cidx = 64 * j + lane, r = cidx / CPR, col = cidx - r * CPR;
+            const int cidx = 64 * j + lane_e, r = cidx / CPR, col = cidx - r * CPR;
             const u32x4 val = *reinterpret_cast<const LDS_AS u32x4*>((const LDS_AS char*)stg +
                                                                      r * RS + col * 16);
             if (row0 + r < Sq) *reinterpret_cast<u32x4*>(Oh + (row0 + r) * a.so.s + col * 8) = val;
@@ -862,14 +941,14 @@ attn_fwd_pipe(const KArgs a) {
     }
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        const int row = qrow0 + 16 * nb;
+        const int row = qrow0e + 16 * nb;
         const float l = quad_group_sum(lacc[nb][0]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         if (row < Sq) {
             T* op = Oh + row * a.so.s;
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) {
-                const int d0 = 16 * ob + 4 * g;
+                const int d0 = 16 * ob + 4 * ge;
                 if (!PAD || d0 < D) {
                     const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
                     const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
@@ -996,19 +1075,33 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
                 for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (key0 + 16 * kb + 4 * g + r >= Skv) S[kb][nb][r] = -INFINITY;
+                        if (key0 + 16 * kb + 4 * (lane_id_here() >> 4) + r >= Skv)
+                            S[kb][nb][r] = -INFINITY;
         }
     };
-    auto lane_max = [&](const f32x4 (&S)[2][2], int nb) __attribute__((always_inline)) {
-        const float mx = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
-        const float my = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
-        return max2(max3(mx, S[1][nb][2], S[1][nb][3]), my);
+    // The lane's largest score over a whole 64-key tile (blocks S and S2).
+    auto lane_max2 = [&](const f32x4 (&S)[2][2], const f32x4 (&S2)[2][2], int nb)
+        __attribute__((always_inline)) {
+        const float a0 = max3(S[0][nb][0], S[0][nb][1], S[0][nb][2]);
+        const float a1 = max3(S[0][nb][3], S[1][nb][0], S[1][nb][1]);
+        const float a2 = max3(S[1][nb][2], S[1][nb][3], S2[0][nb][0]);
+        const float a3 = max3(S2[0][nb][1], S2[0][nb][2], S2[0][nb][3]);
+        const float a4 = max3(S2[1][nb][0], S2[1][nb][1], S2[1][nb][2]);
+        return max2(max3(a0, a1, a2), max3(a3, a4, S2[1][nb][3]));
     };
-    auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2]) __attribute__((always_inline)) {
-        const float lm[2] = {lane_max(S, 0), lane_max(S, 1)};
+    // As attn_fwd_pipe's softmax for D <= 64: the maximum is taken over the
+    // tile's two blocks (S and S2) before the first block's P (S2 non-null)
+    // and not again before the second's (S2 null).
+    auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2])
+        __attribute__((always_inline)) {
+        float lm[2] = {0.f, 0.f};
+        if (S2) {
+            lm[0] = lane_max2(S, *S2, 0);
+            lm[1] = lane_max2(S, *S2, 1);
+        }
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            if (__any(lm[nb] > m_run[nb])) {
+            if (S2 && __any(lm[nb] > m_run[nb])) {
                 const float m_new = max2(m_run[nb], quad_group_max(lm[nb]));
                 const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
 #pragma unroll
@@ -1074,25 +1167,28 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
             mask(Sa, t * C::BN);
             if (t > 0) pv(cur - STAGE, 1, Pb);  // block 2t-1
             qk(cur, 1, Sb);                     // block 2t+1
-            softmax(Sa, Pa);                    // block 2t
             mask(Sb, t * C::BN + 32);
+            softmax(Sa, Pa, &Sb);               // block 2t (max over 2t, 2t+1)
             pv(cur, 0, Pa);                     // block 2t
             qk(nxt, 0, Sa);                     // block 2t+2
-            softmax(Sb, Pb);                    // block 2t+1
+            softmax(Sb, Pb, nullptr);           // block 2t+1
         }
         pv(kv + (ntiles - 1) * STAGE, 1, Pb);  // block 2 ntiles - 1
         }
 
+        // (lane indices recomputed here, see lane_id_here)
+        const int le = lane_id_here(), ge = le >> 4;
+        const int qrow0e = qt * C::BM + wave * 32 + (le & 15);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int row = qrow0 + 16 * nb;
+            const int row = qrow0e + 16 * nb;
             const float l = quad_group_sum(lacc[nb][0]);
             const float inv = l > 0.f ? 1.f / l : 0.f;
             if (row < Sq) {
                 T* op = Oh + row * a.so.s;
 #pragma unroll
                 for (int ob = 0; ob < NOB; ++ob) {
-                    const int d0 = 16 * ob + 4 * g;
+                    const int d0 = 16 * ob + 4 * ge;
                     if (!PAD || d0 < D) {
                         const auto h0 = E::cvt2(oacc[ob][nb][0] * inv, oacc[ob][nb][1] * inv);
                         const auto h1 = E::cvt2(oacc[ob][nb][2] * inv, oacc[ob][nb][3] * inv);
@@ -1965,6 +2061,19 @@ bool d512_wide() {
     return !(env && env[0] == '0' && env[1] == 0);
 }
 
+// D <= 64 ring kernel: keys per workgroup up to which the running max is
+// raised once per 64-key tile (attn_fwd_pipe's TILEMAX). Measured on MI355X
+// against the per-block max (interleaved): c3 (512 keys) +7 %, c1 +3 %,
+// 4096 keys +2.4 %, c5 (131072 keys) -2 %. The K/V-resident kernel (at most
+// 640 keys) always does, and so matches the ring kernel bit for bit. The
+// environment variable GFX906_AMD_ATTN_TILEMAX=0/1 forces either (tests).
+constexpr int kTileMaxKeys = 8192;
+bool tile_max(int keys) {
+    const char* env = getenv("GFX906_AMD_ATTN_TILEMAX");
+    if (env && (env[0] == '0' || env[0] == '1') && env[1] == 0) return env[0] == '1';
+    return keys <= kTileMaxKeys;
+}
+
 template <class T, bool SPLIT>
 void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
     const int D = a.D;
@@ -1978,7 +2087,8 @@ void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
             hipLaunchKernelGGL((attn_fwd_d512<T, false, SPLIT>), grid, dim3(Cfg512::NT), 0, s, a);
     } else if (D == 128) {
         dim3 grid((unsigned)((a.Sq + Cfg128::BM - 1) / Cfg128::BM) * nwg);
-        hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T, SPLIT>), grid, dim3(Cfg128::NT), 0, s, a);
+        hipLaunchKernelGGL((attn_fwd_pipe<Cfg128, false, T, SPLIT, false>), grid, dim3(Cfg128::NT),
+                           0, s, a);
     } else {
         if constexpr (!SPLIT) {
             if (const long long wgs = kvres_grid(a)) {
@@ -1991,10 +2101,19 @@ void launch_kernel(const KArgs& a, unsigned nwg, bool tl, hipStream_t s) {
             }
         }
         dim3 grid((unsigned)((a.Sq + Cfg64::BM - 1) / Cfg64::BM) * nwg);
-        if (D == 64)
-            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T, SPLIT>), grid, dim3(Cfg64::NT), 0, s, a);
+        const bool tm = tile_max(SPLIT ? a.split_len : a.Skv);
+        if (D == 64 && tm)
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T, SPLIT, true>), grid, dim3(Cfg64::NT),
+                               0, s, a);
+        else if (D == 64)
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, false, T, SPLIT, false>), grid,
+                               dim3(Cfg64::NT), 0, s, a);
+        else if (tm)
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T, SPLIT, true>), grid, dim3(Cfg64::NT),
+                               0, s, a);
         else
-            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T, SPLIT>), grid, dim3(Cfg64::NT), 0, s, a);
+            hipLaunchKernelGGL((attn_fwd_pipe<Cfg64, true, T, SPLIT, false>), grid, dim3(Cfg64::NT),
+                               0, s, a);
     }
 }
 

@@ -86,7 +86,7 @@ def counts(body):
     return c
 
 
-KERNELS = r"attn_fwd_pipeINS_3CfgILi128ELi8ELi1EEELb0E(DF16_|DF16b)Lb0EEE"
+KERNELS = r"attn_fwd_pipeINS_3CfgILi128ELi8ELi1EEELb0E(DF16_|DF16b)Lb0ELb0EEE"
 
 
 def test_d128_main_loop_instruction_mix(kernel_asm):
@@ -121,9 +121,9 @@ OCCUPANCY = [("attn_fwd_pipeINS_3CfgILi128", 2), ("attn_fwd_pipeINS_3CfgILi64", 
 
 def test_kernels_do_not_spill(kernel_asm):
     """A scratch reload in a ring kernel's loop comes with a vmcnt(0) wait, which
-    drains the tile loads in flight: no attention kernel may use scratch, except
-    the K/V-resident kernel's one register kept across its work items (stored
-    once before the item loop, reloaded once per item, outside the block loop)."""
+    drains the tile loads in flight: no attention kernel may use scratch. (The
+    D <= 64 kernels run at their 128-VGPR limit; they recompute lane indices
+    after the main loop instead of keeping them in registers across it.)"""
     seen = set()
     for m in RESOURCES.finditer(kernel_asm):
         name, vgprs, scratch, occ = m.group(1), int(m.group(2)), int(m.group(3)), int(m.group(4))
@@ -132,12 +132,7 @@ def test_kernels_do_not_spill(kernel_asm):
             continue
         seen.add(next(pat for pat, _ in OCCUPANCY if pat in name))
         assert occ >= want[0] and vgprs <= 512 // want[0], (name, vgprs, occ)
-        if "attn_fwd_kvres" in name:
-            body = functions(kernel_asm, re.escape(name))[name]
-            assert scratch <= 16, (name, scratch)
-            assert sum(l.lstrip().startswith("scratch_") for l in body) <= 2, name
-        else:
-            assert scratch == 0, (name, scratch)
+        assert scratch == 0, (name, scratch)
     assert seen == {pat for pat, _ in OCCUPANCY}, seen
 
 
