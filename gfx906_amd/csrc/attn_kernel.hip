@@ -698,7 +698,10 @@ attn_fwd_pipe(const KArgs a) {
                 __builtin_amdgcn_exp2f(kLazy ? m_run[nb] - m_new : (m_run[nb] - m_new) * c);
 #pragma unroll
             for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-            lacc[nb] *= alpha;
+            if constexpr (kLazy)
+                lacc[nb] *= alpha;
+            else
+                lacc[nb][0] *= alpha;  // rows 1-3 of the row-sum accumulator stay 0
             m_run[nb] = m_new;
         };
         auto lane_max = [&](const f32x4 (&S)[2][2], int nb) __attribute__((always_inline)) {
@@ -1106,7 +1109,7 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
                 const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
 #pragma unroll
                 for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-                lacc[nb] *= alpha;
+                lacc[nb][0] *= alpha;  // rows 1-3 of the row-sum accumulator stay 0
                 m_run[nb] = m_new;
             }
         }
