@@ -209,18 +209,7 @@ def conv3d_bench(args):
         conv(x, w, b, None, out, dims, xs, os_, [0, 0, 0, 0])
 
     warmup = warm_up(call, args.warmup)
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        call()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms = [s_.elapsed_time(e_) for s_, e_ in zip(starts, ends)]
-    avg = sum(kernel_ms) / len(kernel_ms)
+    avg, wall = time_region(call, args.steps)
     flops = 2 * n * z * p * q * k * c * t ** 3
     achieved = flops / (avg * 1e-3) / 1e12
     print(json.dumps({
@@ -233,7 +222,7 @@ def conv3d_bench(args):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": read_profile_figures(CONV_TRAFFIC_FILE)["traffic"],
-                     "kernel_ms_avg": round(avg, 4), "kernel_ms_min": round(min(kernel_ms), 4),
+                     "kernel_ms_avg": round(avg, 4),
                      "algorithmic_flops_per_launch": flops},
         "cpu_baseline": None if args.no_cpu else conv3d_cpu_baseline(x, w, b)}), flush=True)
 
@@ -272,8 +261,8 @@ def cpu_baseline():
 def torch_sdpa_leg(attn, q, k, v, scale, flops, args):
     """torch.nn.functional.scaled_dot_product_attention with its flash backend
     (else the memory-efficient one; never the math path) on the same contiguous
-    inputs, timed like the kernel: warm-up, then args.steps launches with HIP
-    events on the current stream. None when neither backend serves the call."""
+    inputs, timed like the kernel: warm-up, then args.steps launches between
+    HIP events on the current stream. None when neither backend serves the call."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -285,17 +274,9 @@ def torch_sdpa_leg(attn, q, k, v, scale, flops, args):
                 ref = sdpa(q, k, v, scale=scale)
                 torch.cuda.synchronize()
                 warm_up(lambda: sdpa(q, k, v, scale=scale), args.warmup)
-                stream = torch.cuda.current_stream()
-                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                      for _ in range(args.steps)]
-                for a, b in ev:
-                    a.record(stream)
-                    sdpa(q, k, v, scale=scale)
-                    b.record(stream)
-                torch.cuda.synchronize()
+                avg, _ = time_region(lambda: sdpa(q, k, v, scale=scale), args.steps)
         except RuntimeError:  # backend cannot serve this shape or dtype
             continue
-        avg = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
         achieved = flops / (avg * 1e-3) / 1e12
         return {"backend": backend.name, "kernel_ms_avg": round(avg, 4),
                 "achieved": round(achieved, 2), "frac": round(achieved / PEAK_TFLOPS, 4),
@@ -303,21 +284,26 @@ def torch_sdpa_leg(attn, q, k, v, scale, flops, args):
     return None
 
 
-def time_kernel(call, steps):
-    """Per-launch HIP events on the current stream over `steps` back-to-back
-    launches: (average ms, min ms)."""
+def time_region(call, steps):
+    """`steps` back-to-back launches between two HIP events on the current
+    stream (the stream the kernels run on), bracketed by synchronisations.
+    Returns (average ms per launch from the events, wall-clock seconds of the
+    same region on the host). One event pair over the region, not one per
+    launch: an event between launches adds its own few microseconds to short
+    kernels."""
     import torch
 
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    for a, b in ev:
-        a.record(stream)
-        call()
-        b.record(stream)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    ms = [a.elapsed_time(b) for a, b in ev]
-    return sum(ms) / len(ms), min(ms)
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(steps):
+        call()
+    b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return a.elapsed_time(b) / steps, wall
 
 
 CONFIG_LEGS = ("c2", "c3", "c4", "c5")
@@ -339,14 +325,15 @@ def other_configs(attn, steps):
         scale = D ** -0.5
         flops = gfx906_amd.flops(B, H, Sq, Skv, D)
         warmup = warm_up(lambda: attn(q, k, v, scale), None)
-        avg, best = time_kernel(lambda: attn(q, k, v, scale), steps)
+        avg, _ = time_region(lambda: attn(q, k, v, scale), steps)
         achieved = flops / (avg * 1e-3) / 1e12
         out[name] = {"shape": f"B{B} H{H} Sq{Sq} Skv{Skv} D{D}", "kernel_ms_avg": round(avg, 4),
-                     "kernel_ms_min": round(best, 4), "achieved": round(achieved, 2),
-                     "frac": round(achieved / PEAK_TFLOPS, 4), "warmup": warmup, "steps": steps}
+                     "achieved": round(achieved, 2), "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "warmup": warmup, "steps": steps}
         del q, k, v
     out["measured"] = ("in this run, after the north star's timed region; TFLOP/s from the "
-                       "average kernel time (HIP events), 4*B*H*Sq*Skv*D FLOP per launch")
+                       "average launch time (HIP events over the timed launches), "
+                       "4*B*H*Sq*Skv*D FLOP per launch")
     return out
 
 
@@ -394,20 +381,9 @@ def main():
 
     warmup = warm_up(lambda: attn(q, k, v, scale), args.warmup)
 
-    # Per-launch HIP events on the stream the kernel runs on (the current stream).
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        attn(q, k, v, scale)
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    avg_ms = sum(kernel_ms) / len(kernel_ms)
+    # HIP events on the stream the kernel runs on (the current stream) over
+    # the timed launches, and the host clock over the same region.
+    avg_ms, wall = time_region(lambda: attn(q, k, v, scale), args.steps)
     ms_per_step = wall * 1e3 / args.steps
     value = flops * args.steps / wall / 1e12
     achieved = flops / (avg_ms * 1e-3) / 1e12
@@ -449,7 +425,6 @@ def main():
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": prof["traffic"],
             "kernel_ms_avg": round(avg_ms, 4),
-            "kernel_ms_min": round(min(kernel_ms), 4),
             "algorithmic_flops_per_launch": flops,
             "min_hbm_bytes_per_launch": 2 * (2 * w["B"] * w["H"] * w["Sq"] * w["D"]
                                              + 2 * w["B"] * w["H"] * w["Skv"] * w["D"]),
