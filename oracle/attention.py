@@ -26,8 +26,8 @@ Functions and what pins each one (tests/test_oracle.py):
   model makes (model_check.py:139-153).
 * :func:`kernel_numerics_model` -- the gfx950 kernel's rounding choices
   (fp32 scores and softmax state, fp16-rounded P, row sum taken from the
-  rounded P, the per-head-dim rescale limit taken per wave of 32 rows, fp16
-  output) in numpy. Pinned against :func:`attention_fp64` within the
+  rounded P, the per-head-dim rescale limit taken over the kernel's key
+  tile and row group, fp16 output) in numpy. Pinned against :func:`attention_fp64` within the
   north-star tolerance, and against the one c3 element a stale running max
   moves past the bar; it documents why the kernel's numerics meet the bar,
   it is not what the GPU output is compared with.
@@ -142,18 +142,37 @@ def kernel_tau(D):
     return 0.0 if D <= 64 else (15.0 if D == 128 else 8.0)
 
 
-def kernel_numerics_model(q16, k16, v16, scale, tau=None, tile_n=32, wave_rows=32):
+# Keys over which each kernel takes one rescale decision: the D <= 64 ring
+# kernel raises its running max once per 64-key tile for up to 8192 keys and
+# once per 32-key block above that; D = 128 tests each 32-key block and
+# D = 512 each 32-key tile.
+def kernel_tile(D, Skv):
+    return 64 if D <= 64 and Skv <= 8192 else 32
+
+
+# Query rows that share one rescale decision (the kernels' wave-uniform
+# branch): the D = 128 kernel's wave of 32 rows; the D = 512 kernels decide
+# per 16-row column block (per wave in attn_fwd_d512, per block in
+# attn_fwd_d512w), and D <= 64 per 16-row column block, where with the exact
+# running max the grouping changes nothing (a row whose max did not rise
+# keeps m, and its rescale factor is exactly 1).
+def kernel_wave_rows(D):
+    return 32 if D == 128 else 16
+
+
+def kernel_numerics_model(q16, k16, v16, scale, tau=None, tile_n=None, wave_rows=None):
     """The gfx950 kernel's arithmetic, restated in numpy (float32 state).
 
     Per block of `tile_n` keys: s = q.k in fp32; p = exp2(s*c - m) with the
     running max m (log2 units, c = |scale|*log2e), rounded to fp16. When some
-    rounded p of the block exceeds 2^tau in any of the `wave_rows` rows a wave
-    holds (the kernels' wave-uniform branch), each of those rows takes its
-    exact block max: m' = max(m, max s*c), O and l scale by exp2(m - m') and P
-    is recomputed. Then l += sum(p_fp16), acc += p_fp16 @ v; finally
-    o = fp16(acc * (1/l)). tau defaults to the kernel's limit for the head
-    dim (kernel_tau). Negative scale is applied as (-q, |scale|), exact in
-    fp16.
+    rounded p of the block exceeds 2^tau in any of the `wave_rows` rows that
+    share a decision (the kernels' wave-uniform branch), each of those rows
+    takes its exact block max: m' = max(m, max s*c), O and l scale by
+    exp2(m - m') and P is recomputed. Then l += sum(p_fp16),
+    acc += p_fp16 @ v; finally o = fp16(acc * (1/l)). tau, tile_n and
+    wave_rows default to the kernel's choices for the head dim and key count
+    (kernel_tau, kernel_tile, kernel_wave_rows). Negative scale is applied as
+    (-q, |scale|), exact in fp16.
     """
     q = _as64(q16).astype(np.float32)
     k = _as64(k16).astype(np.float32)
@@ -162,6 +181,8 @@ def kernel_numerics_model(q16, k16, v16, scale, tau=None, tile_n=32, wave_rows=3
         q = -q
     D = q.shape[-1]
     tau = kernel_tau(D) if tau is None else tau
+    tile_n = kernel_tile(D, k.shape[-2]) if tile_n is None else tile_n
+    wave_rows = kernel_wave_rows(D) if wave_rows is None else wave_rows
     c = np.float32(abs(scale) * LOG2E)
     lead, Sq, Skv = q.shape[:-2], q.shape[-2], k.shape[-2]
     m = np.full(q.shape[:-1], -1e30, np.float32)

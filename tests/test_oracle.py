@@ -164,18 +164,42 @@ def test_kernel_numerics_model_meets_tolerance(name, rows):
 
 
 def test_kernel_numerics_model_exact_running_max_on_c3():
-    """c3 head (1, 4): with the D <= 64 kernel's exact running max every
-    element meets the bar; with a lazy max (limit 2^15, the D = 128 policy)
+    """c3 head (1, 4): with the D <= 64 kernel's exact running max (raised
+    once per 64-key tile, or per 32-key block) every element meets the bar;
+    with a lazy max (limit 2^15 tested per 32-key block, the D = 128 policy)
     row 7138 keeps a dominant weight rounded off 1.0 and dim 46 lands past
     2e-3 (the GPU's own output showed the same element, 2.008e-3)."""
     q, k, v = oa.config_inputs("c3")
     q, k, v = q[1:2, 4:5], k[1:2, 4:5], v[1:2, 4:5]
     ref = oa.sdpa_math_fp32(q, k, v, 0.125).numpy()
-    exact = oa.kernel_numerics_model(q, k, v, 0.125)
-    assert np.abs(exact - ref).max() <= oa.MAX_ABS_TOL
-    lazy = oa.kernel_numerics_model(q, k, v, 0.125, tau=15.0)
+    assert oa.kernel_tile(64, 512) == 64
+    for tile_n in (64, 32):
+        exact = oa.kernel_numerics_model(q, k, v, 0.125, tile_n=tile_n)
+        assert np.abs(exact - ref).max() <= oa.MAX_ABS_TOL
+    lazy = oa.kernel_numerics_model(q, k, v, 0.125, tau=15.0, tile_n=32)
     d = np.abs(lazy - ref)
     assert d.max() > oa.MAX_ABS_TOL and np.unravel_index(d.argmax(), d.shape) == (0, 0, 7138, 46)
+
+
+def test_kernel_numerics_model_d512_decides_per_16_rows():
+    """The D = 512 kernels take their rescale decision per 16-row column
+    block: the model over 32 rows equals the model over each 16-row half,
+    also when a key lifts one row of the second half past the 2^8 limit
+    (row 20 scores key 40 at about 2^16). Deciding over all 32 rows, as the
+    D = 128 kernel does, rescales the first half too and changes its bits."""
+    q, k, v = oa.make_inputs(1, 1, 32, 96, 512, 0.5, 0.5, seed=61)
+    q, k = q.float(), k.float()
+    q[0, 0, 20] = 2 * k[0, 0, 40]
+    q, k = q.half(), k.half()
+    s = 512 ** -0.5
+    assert oa.kernel_wave_rows(512) == 16 and oa.kernel_wave_rows(128) == 32
+    full = oa.kernel_numerics_model(q, k, v, s)
+    halves = np.concatenate([oa.kernel_numerics_model(q[:, :, :16], k, v, s),
+                             oa.kernel_numerics_model(q[:, :, 16:], k, v, s)], axis=2)
+    assert np.array_equal(full, halves)
+    assert not np.array_equal(oa.kernel_numerics_model(q, k, v, s, wave_rows=32), halves)
+    ok, mx, mn = oa.within_tolerance(full, oa.attention_fp64(q, k, v, s))
+    assert ok, (mx, mn)
 
 
 def test_kernel_numerics_model_negative_and_zero_scale():
