@@ -938,7 +938,16 @@ attn_fwd_pipe(const KArgs a) {
             const int cidx = 64 * j + lane_e, r = cidx / CPR, col = cidx - r * CPR;
             const u32x4 val = *reinterpret_cast<const LDS_AS u32x4*>((const LDS_AS char*)stg +
                                                                      r * RS + col * 16);
-            if (row0 + r < Sq) *reinterpret_cast<u32x4*>(Oh + (row0 + r) * a.so.s + col * 8) = val;
+            if (row0 + r < Sq) {
+                // D <= 64: non-temporal stores (O is not read again; c3, whose
+                // three rounds of short workgroups store 50 MB, +1.4 %; D = 128
+                // mixed, -0.6 % north star, +1 % c2: not used there).
+                u32x4* dst = reinterpret_cast<u32x4*>(Oh + (row0 + r) * a.so.s + col * 8);
+                if constexpr (DP <= 64)
+                    __builtin_nontemporal_store(val, dst);
+                else
+                    *dst = val;
+            }
         }
         return;
     }
