@@ -767,16 +767,25 @@ attn_fwd_pipe(const KArgs a) {
         // D <= 64 with TILEMAX: P of a tile's two blocks. The first call (S2,
         // the tile's second block, non-null) raises the running max to the
         // max over both blocks, then computes S's P; the second (S2 null)
-        // computes the second block's P with no test.
-        auto softmax_tile = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2])
-            __attribute__((always_inline)) {
+        // computes the second block's P with no test. On the workgroup's first
+        // tile (`first`, wave-uniform) O and l are still exactly zero and the
+        // running max is -inf: the max is raised with no rescale (the rescale
+        // would multiply zeros by exp2(-inf) = 0; c3 rescales on most of its
+        // eight tiles, so this drops about one in seven).
+        auto softmax_tile = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2],
+                                bool first) __attribute__((always_inline)) {
             float lp[2];  // unused: the row sums come from the MFMAs below
             if (S2) {
                 const float lm[2] = {lane_max2(S, *S2, 0), lane_max2(S, *S2, 1)};
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
-                    if (__any(lm[nb] > m_run[nb]))
-                        rescale(nb, max2(m_run[nb], quad_group_max(lm[nb])));
+                    if (__any(lm[nb] > m_run[nb])) {
+                        const float m_new = max2(m_run[nb], quad_group_max(lm[nb]));
+                        if (first)
+                            m_run[nb] = m_new;
+                        else
+                            rescale(nb, m_new);
+                    }
             }
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
@@ -800,7 +809,7 @@ attn_fwd_pipe(const KArgs a) {
             qk(kc, 1, Sb);     // block 2w+1
             if constexpr (kTileMax) {
                 mask(Sb, w * C::BN + 32);
-                softmax_tile(Sa, Pa, &Sb);  // block 2w, max over blocks 2w and 2w+1
+                softmax_tile(Sa, Pa, &Sb, w == 0);  // block 2w, max over blocks 2w and 2w+1
             } else {
                 softmax(Sa, Pa);            // block 2w
             }
@@ -811,7 +820,7 @@ attn_fwd_pipe(const KArgs a) {
             pv(vc, 0, Pa);     // block 2w
             qk(kn, 0, Sa);     // block 2w+2
             if constexpr (kTileMax)
-                softmax_tile(Sb, Pb, nullptr);  // block 2w+1
+                softmax_tile(Sb, Pb, nullptr, false);  // block 2w+1
             else
                 softmax(Sb, Pb);                // block 2w+1
         };
@@ -1103,8 +1112,9 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
     };
     // As attn_fwd_pipe's softmax for D <= 64: the maximum is taken over the
     // tile's two blocks (S and S2) before the first block's P (S2 non-null)
-    // and not again before the second's (S2 null).
-    auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2])
+    // and not again before the second's (S2 null); on an item's first tile
+    // (`first`) it is raised with no rescale of the still-zero O and l.
+    auto softmax = [&](f32x4 (&S)[2][2], x8 (&P)[2], const f32x4 (*S2)[2][2], bool first)
         __attribute__((always_inline)) {
         float lm[2] = {0.f, 0.f};
         if (S2) {
@@ -1115,10 +1125,12 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
         for (int nb = 0; nb < 2; ++nb) {
             if (S2 && __any(lm[nb] > m_run[nb])) {
                 const float m_new = max2(m_run[nb], quad_group_max(lm[nb]));
-                const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
+                if (!first) {
+                    const float alpha = __builtin_amdgcn_exp2f((m_run[nb] - m_new) * c);
 #pragma unroll
-                for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
-                lacc[nb][0] *= alpha;  // rows 1-3 of the row-sum accumulator stay 0
+                    for (int ob = 0; ob < NOB; ++ob) oacc[ob][nb] *= alpha;
+                    lacc[nb][0] *= alpha;  // rows 1-3 of the row-sum accumulator stay 0
+                }
                 m_run[nb] = m_new;
             }
         }
@@ -1180,10 +1192,10 @@ __global__ void __launch_bounds__(CfgRes::NT, 1) attn_fwd_kvres(const KArgs a) {
             if (t > 0) pv(cur - STAGE, 1, Pb);  // block 2t-1
             qk(cur, 1, Sb);                     // block 2t+1
             mask(Sb, t * C::BN + 32);
-            softmax(Sa, Pa, &Sb);               // block 2t (max over 2t, 2t+1)
+            softmax(Sa, Pa, &Sb, t == 0);       // block 2t (max over 2t, 2t+1)
             pv(cur, 0, Pa);                     // block 2t
             qk(nxt, 0, Sa);                     // block 2t+2
-            softmax(Sb, Pb, nullptr);           // block 2t+1
+            softmax(Sb, Pb, nullptr, false);    // block 2t+1
         }
         pv(kv + (ntiles - 1) * STAGE, 1, Pb);  // block 2 ntiles - 1
         }
