@@ -39,6 +39,11 @@ PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
 WORKLOAD = dict(B=1, H=16, Sq=16384, Skv=16384, D=128)
 SEED = 106
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_pmc.txt")
+# Cycles x clock against frac for the north star under the driver's command.
+DRIVER_FORM_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_driver_form.txt")
+DRIVER_FORM_KEYS = ("driver_form_sq_clock_ghz", "driver_form_mfma_busy_pct",
+                    "driver_form_useful_mfma_pct", "driver_form_predicted_frac",
+                    "driver_form_measured_frac")
 CONV_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3d_vae_kernel_trace.txt")
 WARMUP_MS = 250.0  # default warm-up: about this much back-to-back work ...
 MIN_WARMUP = 30  # ... and at least this many launches
@@ -148,6 +153,24 @@ def read_profile_figures(path=TRAFFIC_FILE):
     m = re.search(r"^counters_workload\s*[:=]\s*(.+)$", text, re.M)
     if m:
         out["counters_workload"] = m.group(1).strip()
+    return out
+
+
+def read_driver_form_figures(path=DRIVER_FORM_FILE):
+    """The committed driver-form reconciliation (per-dispatch SQ clock and
+    MFMA-busy cycles against the measured frac), or None without the file."""
+    if not os.path.isfile(path):
+        return None
+    with open(path) as f:
+        text = f.read()
+    out = {}
+    for name in DRIVER_FORM_KEYS:
+        m = re.search(rf"^{name}\s*[:=]\s*([0-9.eE+-]+)", text, re.M)
+        out[name[len("driver_form_"):]] = float(m.group(1)) if m else None
+    out["note"] = ("a profiling session of `bench.py --steps 20 --warmup 5`, not this run: "
+                   "useful = busy x 32/34 (2 of 34 MFMAs per block carry row sums); "
+                   "predicted frac = useful x clock / 2.4 GHz")
+    out["source"] = os.path.relpath(path, ROOT)
     return out
 
 
@@ -433,7 +456,8 @@ def main():
                      "lds_bank_conflict_pct": prof["lds_bank_conflict_pct"],
                      "workload": prof["counters_workload"],
                      "source": os.path.relpath(TRAFFIC_FILE, ROOT)
-                     if north_star and os.path.isfile(TRAFFIC_FILE) else None},
+                     if north_star and os.path.isfile(TRAFFIC_FILE) else None,
+                     "driver_form": read_driver_form_figures() if north_star else None},
     }
     if args.torch_sdpa:
         result["torch_sdpa"] = torch_sdpa_leg(attn, q, k, v, scale, flops, args)

@@ -46,6 +46,19 @@ def test_profile_figures_match_the_committed_summary():
     assert fig["counters_workload"].startswith("ns_h8 (B1 H8 Sq=Skv=16384 D128")
 
 
+def test_driver_form_reconciliation_is_consistent():
+    """The driver-form figures bench.py reports: useful = busy x 32/34, and
+    useful x SQ clock / 2.4 GHz reproduces the measured frac within 1 %."""
+    fig = bench.read_driver_form_figures()
+    assert fig is not None and all(fig[k] is not None for k in
+                                   ("sq_clock_ghz", "mfma_busy_pct", "useful_mfma_pct",
+                                    "predicted_frac", "measured_frac"))
+    assert abs(fig["mfma_busy_pct"] * 32 / 34 - fig["useful_mfma_pct"]) < 0.1
+    pred = fig["useful_mfma_pct"] / 100 * fig["sq_clock_ghz"] / 2.4
+    assert abs(pred - fig["predicted_frac"]) < 2e-3
+    assert abs(fig["predicted_frac"] / fig["measured_frac"] - 1) < 0.01
+
+
 def test_conv_profile_traffic_is_read():
     fig = bench.read_profile_figures(bench.CONV_TRAFFIC_FILE)
     assert fig["traffic"] == 217144832 + 23617536
