@@ -122,6 +122,10 @@ struct KArgs {
     // (measured: +1 % north star and c2; with 512 keys the two extra
     // barriers cost more than the gathered global loads).
     int q_lds;
+    // Compute units of the device: with the kernel's workgroups per CU, how
+    // many workgroups are resident at once (the D <= 128 kernels prefetch the
+    // Q tile of the workgroup that starts after them into L2).
+    int ncu;
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -488,6 +492,8 @@ attn_fwd_pipe(const KArgs a) {
     __shared__ __attribute__((aligned(1024))) char v1[TILE];
     __shared__ __attribute__((aligned(1024))) char v2[TILE];
     __shared__ __attribute__((aligned(1024))) char v3[TILE];
+    // Destination of the Q prefetch below (never read).
+    __shared__ __attribute__((aligned(256))) char qpf[C::NW * 256];
 
     const int Sq = a.Sq, D = a.D;
     const float c = a.c;
@@ -603,6 +609,45 @@ attn_fwd_pipe(const KArgs a) {
                 asm volatile("" : "+v"(vaddr[ob]));
             }
         }
+
+        // L2 prefetch of the Q tile of the workgroup that starts after this
+        // one on the same XCD: with R = CUs x workgroups per CU resident,
+        // workgroup blockIdx + R (R a multiple of 8, so the same XCD, whose L2
+        // it then reads). Issued in the last group of four key tiles, so the
+        // lines arrive while this workgroup finishes, instead of as a burst of
+        // every new workgroup's Q loads at once. One dword per 128-byte line,
+        // through a range-checked descriptor into a scratch LDS area that is
+        // never read: no fault past the tensor, no registers held. Every wave
+        // issues exactly one such load whether or not there is a workgroup to
+        // prefetch for (then through an empty range: no memory access), since
+        // the waits of the group's next two tiles count it.
+        auto prefetch_next_q = [&]() __attribute__((always_inline)) {
+            const long long resident = (long long)a.ncu * C::OCC;
+            const long long nb = (long long)blockIdx.x + resident;
+            const long long span = (long long)(C::BM - 1) * a.sq.s * 2 + DP * 2;
+            const T* base = (const T*)a.q;
+            int bytes = 0, off = 0;
+            if (resident > 0 && (resident & 7) == 0 && nb < (long long)gridDim.x &&
+                span < (1LL << 31)) {  // (uniform)
+                int w2 = (int)nb;
+                if ((gridDim.x & 7) == 0) w2 = (w2 & 7) * (int)(gridDim.x >> 3) + (w2 >> 3);
+                const int qt2 = w2 % nqt;
+                int bh2 = w2 / nqt;
+                if constexpr (SPLIT) bh2 /= a.nsplit;
+                const int b2 = bh2 / a.H, h2 = bh2 - b2 * a.H;
+                const int rows = min(Sq - qt2 * C::BM, C::BM);
+                bytes = (int)((rows - 1) * a.sq.s * 2 + D * 2);
+                base += b2 * a.sq.b + h2 * a.sq.h + (long long)qt2 * C::BM * a.sq.s;
+                constexpr int LPR = DP * 2 / 128;         // 128-byte lines per row
+                constexpr int LPW = C::BM * LPR / C::NW;  // lines per wave (64 or 32)
+                const int l = wave * LPW + (lane_id_here() & (LPW - 1));
+                off = (int)((l / LPR) * a.sq.s * 2) + (l % LPR) * 128;
+            }
+            const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)base, 0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)(qpf + wave * 256), 4, off,
+                                                     0, 0, 0);
+        };
 
         // PV MFMAs left to the QK^T step that follows (see pv; for D = 64,
         // 2 and 4 measured -0.5 and -1.2 % on c5).
@@ -801,9 +846,13 @@ attn_fwd_pipe(const KArgs a) {
 
         // Tile w (blocks 2w, 2w+1) in stage cur (K tile kc, V tile vc); vp
         // holds V of tile w-1, kn K of tile w+1; the stage of tile w-1 (kf,
-        // vf) takes tile w+3.
-        auto tile = [&](int w, const char* vp, const char* kc, const char* vc, const char* kn,
-                        char* kf, char* vf) __attribute__((always_inline)) {
+        // vf) takes tile w+3. PF: issue the Q prefetch after tile w+3's loads;
+        // EX: one prefetch load younger than tile w+1's loads is in flight
+        // (the wait leaves it).
+        auto tile = [&](auto pf, auto ex, int w, const char* vp, const char* kc, const char* vc,
+                        const char* kn, char* kf, char* vf) __attribute__((always_inline)) {
+            constexpr bool PF = decltype(pf)::value;
+            constexpr int EX = decltype(ex)::value;
             mask(Sa, w * C::BN);
             pv(vp, 1, Pb);     // block 2w-1
             qk(kc, 1, Sb);     // block 2w+1
@@ -813,9 +862,10 @@ attn_fwd_pipe(const KArgs a) {
             } else {
                 softmax(Sa, Pa);            // block 2w
             }
-            __builtin_amdgcn_s_waitcnt(kWaitNext);  // own loads of tile w+1 done
-            lds_barrier();                          // every wave's; tile w-1 consumed
+            __builtin_amdgcn_s_waitcnt(kWaitNext + EX);  // own loads of tile w+1 done
+            lds_barrier();                               // every wave's; tile w-1 consumed
             issue(w + 3, kf, vf);
+            if constexpr (PF) prefetch_next_q();
             if constexpr (!kTileMax) mask(Sb, w * C::BN + 32);
             pv(vc, 0, Pa);     // block 2w
             qk(kn, 0, Sa);     // block 2w+2
@@ -873,13 +923,30 @@ attn_fwd_pipe(const KArgs a) {
 
         // Whole groups of four tiles (tiles past the end hold zeros and are
         // masked to p = 0); a single exit keeps the loop's register
-        // allocation intact.
+        // allocation intact. With kPrefetchQ the last group issues the Q
+        // prefetch in its first tile; the waits of its next two tiles leave
+        // that load in flight, the last tile's wait (for loads issued after
+        // it) takes it. Not for D <= 64 without the tile max (long key
+        // ranges, where the prefetch would save a negligible share and its
+        // second copy of the group makes the kernel spill at 128 VGPRs).
+        constexpr bool kPrefetchQ = kLazy || kTileMax;
+        using B0 = std::integral_constant<bool, false>;
+        using B1 = std::integral_constant<bool, true>;
+        using E0 = std::integral_constant<int, 0>;
+        using E1 = std::integral_constant<int, 1>;
         for (int w0 = 0;; w0 += 4) {
-            tile(w0 + 0, v3, k0, v0, k1, k3, v3);
-            tile(w0 + 1, v0, k1, v1, k2, k0, v0);
-            tile(w0 + 2, v1, k2, v2, k3, k1, v1);
-            tile(w0 + 3, v2, k3, v3, k0, k2, v2);
-            if (w0 + 4 >= ntiles) break;
+            if (kPrefetchQ && w0 + 4 >= ntiles) {
+                tile(B1{}, E0{}, w0 + 0, v3, k0, v0, k1, k3, v3);
+                tile(B0{}, E1{}, w0 + 1, v0, k1, v1, k2, k0, v0);
+                tile(B0{}, E1{}, w0 + 2, v1, k2, v2, k3, k1, v1);
+                tile(B0{}, E0{}, w0 + 3, v2, k3, v3, k0, k2, v2);
+                break;
+            }
+            tile(B0{}, E0{}, w0 + 0, v3, k0, v0, k1, k3, v3);
+            tile(B0{}, E0{}, w0 + 1, v0, k1, v1, k2, k0, v0);
+            tile(B0{}, E0{}, w0 + 2, v1, k2, v2, k3, k1, v1);
+            tile(B0{}, E0{}, w0 + 3, v2, k3, v3, k0, k2, v2);
+            if (!kPrefetchQ && w0 + 4 >= ntiles) break;
         }
         pv(v3, 1, Pb);   // block 2w+1 of the last tile
         // The zero-range loads past the end must land before the workgroup's
@@ -2476,6 +2543,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     a.ws_ml = nullptr;
     a.o16 = (uintptr_t)o % 16 == 0 && so.b % 8 == 0 && so.h % 8 == 0 && so.s % 8 == 0 && so.d == 1;
     a.q_lds = sq.s <= (1LL << 24) && Skv > 1024;
+    a.ncu = cu_count();
     SplitPlan p{1, 0};
     if (workspace_bytes != (size_t)-1)  // split the keys if it pays
         p = plan_split(B, H, Sq, Skv, D, use_scratch ? kScratchBytes : (size_t)-1);
