@@ -155,7 +155,8 @@ def test_tiled_online_softmax_rising_scores():
 @pytest.mark.parametrize("name,rows", [("c1", 1024), ("c3", 64), ("c2", 32)])
 def test_kernel_numerics_model_meets_tolerance(name, rows):
     """The gfx950 kernel's rounding design stays inside the north-star bar on
-    row slices of the BASELINE configs (c3 is the binding one, survey 8c)."""
+    row slices of the BASELINE configs (c3 is the binding one: its sharp rows reach
+    |o| > 4, where fp16 output rounding alone takes up to 1.95e-3 of the 2e-3 budget)."""
     B, H, Sq, Skv, D, qm, vm, seed = oa.CONFIGS[name]
     q, k, v = oa.make_inputs(B, min(H, 2), min(Sq, rows), Skv, D, qm, vm, seed)
     out = oa.kernel_numerics_model(q, k, v, D ** -0.5)
