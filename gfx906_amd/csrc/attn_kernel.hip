@@ -123,8 +123,9 @@ struct KArgs {
     // barriers cost more than the gathered global loads).
     int q_lds;
     // Compute units of the device: with the kernel's workgroups per CU, how
-    // many workgroups are resident at once (the D <= 128 kernels prefetch the
-    // Q tile of the workgroup that starts after them into L2).
+    // many workgroups are resident at once (the D = 128 ring kernel and the
+    // D <= 64 one with the tile max prefetch the Q tile of the workgroup that
+    // starts after them into L2).
     int ncu;
 };
 
