@@ -11,10 +11,11 @@ resident in HBM. Prints one JSON line with the driver's fields plus:
   ``traffic`` is the HBM bytes per launch read from the committed rocprofv3
   counter summary (profiles/), or null when that file is absent.
 * ``counters``: MFMA busy % and LDS bank-conflict % from the committed
-  rocprofv3 summary, with the workload they were measured on.
+  rocprofv3 summary, with the workload they were measured on, and
+  ``driver_form``: the committed per-dispatch reconciliation of this command's
+  short form (SQ clock x useful MFMA cycles against the measured frac).
 * ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine)
   over the whole workload, chunked by head and 2048 query rows.
-
 * ``configs``: kernel rates of BASELINE.json's configs c2-c5, each timed the
   same way after the north star's timed region (not part of it).
 
