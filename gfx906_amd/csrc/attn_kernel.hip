@@ -119,8 +119,10 @@ struct KArgs {
     int o16;
     // Load Q through LDS, as K (whole rows), in the D = 64 and 128 kernels:
     // set for q sequence strides up to 2^24 elements and more than 1024 keys
-    // (measured: +1 % north star and c2; with 512 keys the two extra
-    // barriers cost more than the gathered global loads).
+    // for D <= 64, 256 for D = 128 (measured: +1 % north star and c2; at 512
+    // keys, with the Q tile prefetched into L2, D = 128 +1.1 % and D = 64 +-0,
+    // where before the prefetch the two extra barriers cost more than the
+    // gathered global loads).
     int q_lds;
     // Compute units of the device: with the kernel's workgroups per CU, how
     // many workgroups are resident at once (the D = 128 ring kernel and the
@@ -2543,7 +2545,7 @@ int attn_fwd_impl(const void* q, const void* k, const void* v, void* o, int B, i
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
     a.o16 = (uintptr_t)o % 16 == 0 && so.b % 8 == 0 && so.h % 8 == 0 && so.s % 8 == 0 && so.d == 1;
-    a.q_lds = sq.s <= (1LL << 24) && Skv > 1024;
+    a.q_lds = sq.s <= (1LL << 24) && Skv > (D == 128 ? 256 : 1024);
     a.ncu = cu_count();
     SplitPlan p{1, 0};
     if (workspace_bytes != (size_t)-1)  // split the keys if it pays

@@ -379,14 +379,15 @@ def test_runs_on_current_stream():
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D,Skv", [(64, 1500), (128, 1500), (128, 300), (64, 300)])
 @pytest.mark.parametrize("Sq,scale_sign,q_layout", [(300, 1, "contig"), (1000, -1, "bshd"),
                                                     (257, 1, "bshd"), (33, -1, "contig")])
-def test_long_key_range_q_through_lds(D, Sq, scale_sign, q_layout):
-    """More than 1024 keys: Q goes through LDS as K-shaped tiles (rows past Sq
-    load zeros, the sign of a negative scale applied after the read, any q
-    sequence stride up to 2^24)."""
-    B, H, Skv = 1, 3, 1500
+def test_long_key_range_q_through_lds(D, Skv, Sq, scale_sign, q_layout):
+    """More than 1024 keys (D <= 64) or 256 keys (D = 128): Q goes through LDS
+    as K-shaped tiles (rows past Sq load zeros, the sign of a negative scale
+    applied after the read, any q sequence stride up to 2^24); D = 64 with 300
+    keys takes the gathered global loads, for comparison."""
+    B, H = 1, 3
     q, k, v = make_inputs(B, H, Sq, Skv, D, seed=D + Sq)
     scale = scale_sign * D ** -0.5
     if q_layout == "bshd":
