@@ -303,6 +303,30 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
     return __builtin_bit_cast(typename Elem<T>::x8, __builtin_bit_cast(u32x4, val) ^ qneg);
 }
 
+// Q rows of one workgroup through a range-checked buffer descriptor: the
+// loads are unconditional (no per-row branch, so the compiler does not merge
+// them with a zero value through copies that wait for the data), and rows
+// past `valid_rows` or offsets past the range (kQOutOfRange) read as zeros.
+// The caller applies the sign of a negative scale later, once the prologue
+// waits for its loads anyway: an XOR right after the loads would hold back
+// every later load of the prologue behind them.
+constexpr unsigned kQOutOfRange = 0x80000000u;
+template <class T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t q_rsrc(const T* row0, int valid_rows, long long ss,
+                                                        int D) {
+    const int bytes = valid_rows > 0 ? (int)(((valid_rows - 1) * ss + D) * 2) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)row0, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+template <class T>
+__device__ __forceinline__ typename Elem<T>::x8 q_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(typename Elem<T>::x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+template <class X8>
+__device__ __forceinline__ void q_negate(X8& f, unsigned qneg) {
+    f = __builtin_bit_cast(X8, __builtin_bit_cast(u32x4, f) ^ qneg);
+}
+
 // Whether some element of a block's rounded P (two 8-element operands, all
 // non-negative) exceeds `lim` or is NaN, in any lane of the wave. The first
 // block (running max -1e30, p = inf) always does. A tree of
@@ -532,15 +556,33 @@ attn_fwd_pipe(const KArgs a) {
     x8 qf[2][NQF];
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
     const bool q_lds = !PAD && a.q_lds && ntiles > 0;
+    // Register path: the sign of a negative scale is applied after the
+    // prologue's barrier (q_negate below), so that the Q loads overlap the
+    // first K/V tiles' instead of being waited for before those are issued.
     if (!q_lds) {
+        const int qrows = min(Sq - qt * C::BM, C::BM);
+        if ((long long)(C::BM - 1) * a.sq.s * 2 + DP * 2 < (1LL << 31)) {  // (uniform)
+            const __amdgpu_buffer_rsrc_t qr = q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+            for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int s = 0; s < NQF; ++s) {
-                const int d0 = 32 * s + 8 * g, row = qrow0 + 16 * nb;
-                qf[nb][s] =
-                    q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), qneg);
-            }
+                for (int s = 0; s < NQF; ++s) {
+                    const int d0 = 32 * s + 8 * g, r = wave * 32 + 16 * nb + i;
+                    const unsigned off = r < qrows && (!PAD || d0 < D)
+                                             ? (unsigned)((r * a.sq.s + d0) * 2)
+                                             : kQOutOfRange;
+                    qf[nb][s] = q_load<T>(qr, off);
+                }
+        } else {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int s = 0; s < NQF; ++s) {
+                    const int d0 = 32 * s + 8 * g, row = qrow0 + 16 * nb;
+                    qf[nb][s] =
+                        q_fragment(Qh + row * a.sq.s + d0, row < Sq && (!PAD || d0 < D), 0u);
+                }
+        }
     }
 
     f32x4 oacc[NOB][2];
@@ -921,6 +963,12 @@ attn_fwd_pipe(const KArgs a) {
             *reinterpret_cast<u32x4*>(v3 + 16 * z) = u32x4{};
         __builtin_amdgcn_s_waitcnt(kWaitNext);
         lds_barrier();
+        if (!q_lds && qneg) {  // (uniform)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int s = 0; s < NQF; ++s) q_negate(qf[nb][s], qneg);
+        }
         issue(2, k2, v2);
         qk(k0, 0, Sa);
 
@@ -1770,21 +1818,43 @@ attn_fwd_d512w(const KArgs a) {
 
     // Q^T fragments (B operands: column = query 16rb + l%16, k = dims
     // 32s + 8(l/16)..+7).
-    // Issue order K(0), Q, V(0), K(1): the prologue waits for the first two.
-    if (ntiles > 0) issue(Kh, kss, 0, kb0);
+    // Issue order Q, K(0), V(0), K(1): the prologue waits for the first two.
+    // Q goes through a range-checked descriptor where the workgroup's rows
+    // span less than 2 GiB; the sign of a negative scale is applied after the
+    // prologue's barrier, so that no wait for Q comes before the tiles are
+    // issued. (With the predicated fallback for larger spans, the compiler
+    // waits for every load in flight before the descriptor loads, so nothing
+    // is issued before Q.)
     x8 qf[2][NQF];
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
+    if ((long long)(C::BM - 1) * a.sq.s * 2 + D * 2 < (1LL << 31)) {  // (uniform)
+        const int qrows = ntiles > 0 ? min(Sq - qt * C::BM, C::BM) : 0;
+        const __amdgpu_buffer_rsrc_t qr = q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int s = 0; s < NQF; ++s) {
-            const int row = qrow0 + 16 * rb;
-            qf[rb][s] = q_fragment(Qh + row * a.sq.s + 32 * s + 8 * g, row < Sq && ntiles > 0, qneg);
-        }
-    if (ntiles > 0) {
-        issue(Vh, vss, 0, vb0);
-        issue(Kh, kss, 1, kb1);
+            for (int s = 0; s < NQF; ++s) {
+                const int r = wave * 32 + 16 * rb + i;
+                const unsigned off =
+                    r < qrows ? (unsigned)((r * a.sq.s + 32 * s + 8 * g) * 2) : kQOutOfRange;
+                qf[rb][s] = q_load<T>(qr, off);
+            }
+    } else {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int s = 0; s < NQF; ++s) {
+                const int row = qrow0 + 16 * rb;
+                qf[rb][s] = q_fragment(Qh + row * a.sq.s + 32 * s + 8 * g, row < Sq && ntiles > 0, 0u);
+            }
     }
+    // Issued whatever the key count (with no keys the descriptors are empty
+    // and the wait after the loop covers them): loads under a condition here
+    // make the compiler assume, after the barrier, that the Q loads may be
+    // the last ones issued, and wait for V(0) and K(1) in the first QK^T.
+    issue(Kh, kss, 0, kb0);
+    issue(Vh, vss, 0, vb0);
+    issue(Kh, kss, 1, kb1);
 
     // K read: row 16kb + i, dims 32s + 8g..; V^T read (transposed, per
     // 16-lane group g): rows 4g + i/4 and 16 + 4g + i/4, dims 16ob + 4(i%4)..
@@ -1959,6 +2029,12 @@ attn_fwd_d512w(const KArgs a) {
         // of tile 0 and their exact max.
         __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
         lds_barrier();
+        if (qneg) {  // (uniform)
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int s = 0; s < NQF; ++s) q_negate(qf[rb][s], qneg);
+        }
         qk(kb0, S);
         if (BN > Skv) mask_tail(0, S);
 #pragma unroll
@@ -1971,8 +2047,8 @@ attn_fwd_d512w(const KArgs a) {
             iter(t, kb0, kb1, vb0, vb1);
             if (t + 1 < ntiles) iter(t + 1, kb1, kb0, vb1, vb0);
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the (empty) loads past the end
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the (empty) loads past the end
 
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
