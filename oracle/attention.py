@@ -34,6 +34,10 @@ Functions and what pins each one (tests/test_oracle.py):
 * :func:`chunked_sdpa_math` -- :func:`sdpa_math_fp32` over head / row
   blocks, bounding memory for long sequences; pinned against the unchunked
   call.
+* :func:`within_rounded_tolerance` -- the north-star bars where the output
+  format's spacing allows them, else half an ulp plus the mean bar, element
+  by element; pinned by correctly rounded fp16 values, the per-magnitude
+  limits of fp16 and bf16 and the seeded sweep's rounding-boundary element.
 
 Skv == 0: every function returns zeros (torch SDPA MATH on CPU returns zeros
 for an empty key set; the reference kernel leaves those rows unwritten).
@@ -225,6 +229,29 @@ def error_stats(out, ref):
 def within_tolerance(out, ref, max_tol=MAX_ABS_TOL, mean_tol=MEAN_ABS_TOL):
     mx, mn = error_stats(out, ref)
     return mx <= max_tol and mn <= mean_tol, mx, mn
+
+
+# Significant bits of the output formats (implicit bit included).
+OUT_BITS = {"fp16": 11, "bf16": 8}
+
+
+def within_rounded_tolerance(out, ref, fmt="fp16", mult=1.0):
+    """The north-star bars (times `mult`) for an output stored in `fmt`, where
+    that format's own spacing allows them: element by element, the error may
+    instead reach half a unit in the last place of `ref` in `fmt` plus the
+    mean bar. An fp16 output with |o| >= 4 errs by up to 1.95e-3 when
+    correctly rounded, so an absolute 2e-3 would leave 5e-5 for everything
+    before the rounding; below 4 (fp16) the bar is the plain one. Returns
+    (ok, max-abs, mean-abs); the mean bar applies unchanged."""
+    o, r = _as64(out), _as64(ref)
+    d = np.abs(o - r)
+    if d.size == 0:
+        return True, 0.0, 0.0
+    _, e = np.frexp(np.abs(r))  # |r| = f * 2^e, f in [0.5, 1)
+    half_ulp = np.ldexp(1.0, np.maximum(e - OUT_BITS[fmt] - 1, -149))
+    allowed = np.maximum(half_ulp + mult * MEAN_ABS_TOL, mult * MAX_ABS_TOL)
+    return bool((d <= allowed).all()) and float(d.mean()) <= mult * MEAN_ABS_TOL, \
+        float(d.max()), float(d.mean())
 
 
 # ---------------------------------------------------------------------------

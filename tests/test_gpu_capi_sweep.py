@@ -17,7 +17,12 @@ of either sign, and a layout per tensor (contiguous, [B, S, H, D] transpose,
 padded sequence stride, K/V shared by every head with head stride 0, and for
 D = 512 the token-contiguous K/V of a [b, c, h*w] activation). Outputs of the
 first two calls are held to the bars of the other parity tests against SDPA
-MATH in fp32 on the CPU. Each case prints its parameters first.
+MATH in fp32 on the CPU (fp16 2e-3 / 2e-4, bf16 eight times that), except
+where the output format's spacing leaves no room under the max bar: there an
+element may be off by half a unit in the last place of the reference plus the
+mean bar (within_rounded_tolerance; fp16 from |o| >= 4, where the correctly
+rounded output alone errs by up to 1.95e-3). Each case prints its parameters
+first.
 """
 
 import ctypes
@@ -28,7 +33,7 @@ import pytest
 import torch
 
 import gfx906_amd
-from oracle.attention import make_inputs, sdpa_math_fp32, within_tolerance
+from oracle.attention import make_inputs, sdpa_math_fp32, within_rounded_tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -36,16 +41,6 @@ pytestmark = pytest.mark.gpu
 N_CASES = int(os.environ.get("GFX906_AMD_CAPI_SWEEP_CASES", "48"))
 HEAD_DIMS = [8, 24, 40, 56, 64, 64, 128, 128, 128, 512, 512]
 F16, BF16 = 0, 1
-
-
-def bf16_ok(out, ref):
-    """bf16 bar: eight times the fp16 bars, or the bf16 rounding of a value
-    within the mean bar where the bf16 spacing alone exceeds the max bar."""
-    d = (out.float().cpu() - ref).abs()
-    _, e = torch.frexp(ref.abs())
-    half_ulp = torch.ldexp(torch.ones_like(ref), (e - 9).clamp(min=-133))
-    allowed = torch.clamp(half_ulp + 8 * 2e-4, min=8 * 2e-3)
-    return bool((d <= allowed).all()) and d.mean().item() <= 8 * 2e-4, d.max().item(), d.mean().item()
 
 
 def strides(t):
@@ -133,8 +128,8 @@ def test_capi_random_case(lib, i):
     ref = sdpa_math_fp32(q.contiguous(), k.contiguous(), v.contiguous(), c["scale"])
     for name, o in (("ex", outs[0]), ("split", outs[1])):
         if c["dtype"] == torch.float16:
-            ok, mx, mn = within_tolerance(o.float().cpu(), ref)
+            ok, mx, mn = within_rounded_tolerance(o.float().cpu(), ref, "fp16")
         else:
-            ok, mx, mn = bf16_ok(o, ref)
+            ok, mx, mn = within_rounded_tolerance(o.float().cpu(), ref, "bf16", mult=8)
         print(f"  {name} (workspace {need} B): max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
         assert ok, (name, c, mx, mn)

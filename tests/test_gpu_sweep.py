@@ -9,31 +9,28 @@ and a layout per tensor: contiguous, the DiT [B, S, H, D] transpose, a
 padded sequence stride, K/V broadcast over heads, or (D = 512) the VAE's
 token-contiguous K/V view; the output is allocated by the op, or written into
 a [B, S, H, D] or padded view. The bars are those of the other parity tests:
-fp16 max-abs <= 2e-3 and mean-abs <= 2e-4; bf16 eight times that, or the bf16
-rounding of a value within the mean bar where the bf16 spacing alone exceeds
-the max bar.
+fp16 max-abs <= 2e-3 and mean-abs <= 2e-4; bf16 eight times that. Where the
+output format's own spacing leaves no room under the max bar (fp16 |o| >= 4,
+where the correctly rounded output alone errs by up to 1.95e-3; bf16 from
+|o| >= 4 at its bar), an element may instead be off by half a unit in the
+last place of the reference plus the mean bar (within_rounded_tolerance).
+GFX906_AMD_SWEEP_CASES=n runs a longer sweep (same generator, more seeds).
 """
+
+import os
 
 import numpy as np
 import pytest
 import torch
 
 import gfx906_amd
-from oracle.attention import make_inputs, sdpa_math_fp32, within_tolerance
+from oracle.attention import make_inputs, sdpa_math_fp32, within_rounded_tolerance
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-N_CASES = 100
+N_CASES = int(os.environ.get("GFX906_AMD_SWEEP_CASES", "100"))
 HEAD_DIMS = [8, 16, 24, 32, 40, 48, 56, 64, 64, 128, 128, 128, 512, 512]
-
-
-def bf16_ok(out, ref):
-    d = (out.float().cpu() - ref).abs()
-    _, e = torch.frexp(ref.abs())
-    half_ulp = torch.ldexp(torch.ones_like(ref), (e - 9).clamp(min=-133))
-    allowed = torch.clamp(half_ulp + 8 * 2e-4, min=8 * 2e-3)
-    return bool((d <= allowed).all()) and d.mean().item() <= 8 * 2e-4, d.max().item(), d.mean().item()
 
 
 def place(x, how, rng):
@@ -101,8 +98,8 @@ def test_random_case(i):
         assert got.data_ptr() == out.data_ptr()
     ref = sdpa_math_fp32(q.contiguous(), k.contiguous(), v.contiguous(), c["scale"])
     if c["dtype"] == torch.float16:
-        ok, mx, mn = within_tolerance(got.float().cpu(), ref)
+        ok, mx, mn = within_rounded_tolerance(got.float().cpu(), ref, "fp16")
     else:
-        ok, mx, mn = bf16_ok(got, ref)
+        ok, mx, mn = within_rounded_tolerance(got.float().cpu(), ref, "bf16", mult=8)
     print(f"case {i}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
     assert ok, (c, mx, mn)

@@ -150,6 +150,50 @@ def test_tiled_online_softmax_rising_scores():
                                oa.attention_fp64(q, k, v, 0.5), atol=1e-12)
 
 
+# -- within_rounded_tolerance --------------------------------------------------------
+
+def one(out_val, ref_val, fmt="fp16", mult=1.0):
+    """The bar on one element among 999 exact zeros (so the mean bar does not bind)."""
+    ref = np.zeros(1000)
+    out = np.zeros(1000)
+    ref[0], out[0] = ref_val, out_val
+    return oa.within_rounded_tolerance(out, ref, fmt, mult)[0]
+
+
+def test_rounded_tolerance_takes_the_output_format_spacing():
+    """Correctly rounded fp16 values pass element by element (the plain 2e-3 bar
+    fails them from |o| >= 8, where half an fp16 ulp is 3.9e-3); below |o| = 4
+    the bar is the plain 2e-3; from 4 to 8 it is half an ulp (1.95e-3) plus the
+    mean bar, which passes the seeded sweep's element whose exact value,
+    4.037011, lies 1e-4 below the midpoint of 4.0352 and 4.0391, and one ulp
+    further fails. The mean bar is unchanged."""
+    rng = np.random.default_rng(3)
+    # a few large values among many exact small ones (a mean like an output's)
+    ref = np.concatenate([rng.uniform(-12, 12, 96), rng.integers(-256, 256, 4000) / 256])
+    rounded = ref.astype(np.float16).astype(np.float64)
+    assert oa.within_rounded_tolerance(rounded, ref, "fp16")[0]
+    assert not oa.within_tolerance(rounded, ref)[0]
+    for small in (1.0, 3.9, -2.5):
+        assert one(small + 1.9e-3, small) and not one(small + 2.1e-3, small)
+    assert one(4.039062, 4.037011) and 4.039062 - 4.037011 > 2e-3
+    assert not one(4.039062 + 2 ** -8, 4.037011)
+    assert one(8.0 + 3.8e-3, 8.0) and not one(8.0 + 4.2e-3, 8.0)  # half ulp 3.9e-3 + 2e-4
+    errs = np.full(50, 2.5e-4)
+    assert not oa.within_rounded_tolerance(np.ones(50) + errs, np.ones(50), "fp16")[0]
+
+
+def test_rounded_tolerance_bf16_form():
+    """bf16 at eight times the bars: half a bf16 ulp (8 significant bits) plus
+    1.6e-3, at least 1.6e-2, element by element; the mean bar 1.6e-3."""
+    for ref, half_ulp in ((0.5, 2 ** -9), (3.0, 2 ** -7), (7.5, 2 ** -6), (12.0, 2 ** -5),
+                          (100.0, 2 ** -2)):
+        allowed = max(half_ulp + 8 * 2e-4, 8 * 2e-3)
+        assert one(ref + 0.99 * allowed, ref, "bf16", 8), ref
+        assert not one(ref + 1.01 * allowed, ref, "bf16", 8), ref
+    assert not oa.within_rounded_tolerance(np.full(50, 1.0 + 1.7e-3), np.ones(50), "bf16",
+                                           mult=8)[0]
+
+
 # -- kernel_numerics_model -------------------------------------------------------
 
 @pytest.mark.parametrize("name,rows", [("c1", 1024), ("c3", 64), ("c2", 32)])
