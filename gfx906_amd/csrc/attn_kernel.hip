@@ -312,15 +312,16 @@ __device__ __forceinline__ typename Elem<T>::x8 q_fragment(const T* p, bool load
 // every later load of the prologue behind them.
 constexpr unsigned kQOutOfRange = 0x80000000u;
 template <class T>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t q_rsrc(const T* row0, int valid_rows, long long ss,
-                                                        int D) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t q_rsrc(const T* row0, int valid_rows,
+                                                        long long ss, int D) {
     const int bytes = valid_rows > 0 ? (int)(((valid_rows - 1) * ss + D) * 2) : 0;
     return __builtin_amdgcn_make_buffer_rsrc((void*)row0, 0, __builtin_amdgcn_readfirstlane(bytes),
                                              0x00020000);
 }
 template <class T>
 __device__ __forceinline__ typename Elem<T>::x8 q_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(typename Elem<T>::x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return __builtin_bit_cast(typename Elem<T>::x8,
+                              __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 template <class X8>
 __device__ __forceinline__ void q_negate(X8& f, unsigned qneg) {
@@ -562,7 +563,8 @@ attn_fwd_pipe(const KArgs a) {
     if (!q_lds) {
         const int qrows = min(Sq - qt * C::BM, C::BM);
         if ((long long)(C::BM - 1) * a.sq.s * 2 + DP * 2 < (1LL << 31)) {  // (uniform)
-            const __amdgpu_buffer_rsrc_t qr = q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
+            const __amdgpu_buffer_rsrc_t qr =
+                q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -1829,7 +1831,8 @@ attn_fwd_d512w(const KArgs a) {
     const unsigned qneg = a.qsign < 0.f ? 0x80008000u : 0u;
     if ((long long)(C::BM - 1) * a.sq.s * 2 + D * 2 < (1LL << 31)) {  // (uniform)
         const int qrows = ntiles > 0 ? min(Sq - qt * C::BM, C::BM) : 0;
-        const __amdgpu_buffer_rsrc_t qr = q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
+        const __amdgpu_buffer_rsrc_t qr =
+            q_rsrc(Qh + (long long)qt * C::BM * a.sq.s, qrows, a.sq.s, D);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
