@@ -10,6 +10,8 @@ resident in HBM. Prints one JSON line with the driver's fields plus:
   on the stream the kernel runs on, against MI355X's dense fp16 MFMA peak;
   ``traffic`` is the HBM bytes per launch read from the committed rocprofv3
   counter summary (profiles/), or null when that file is absent.
+* ``launches``: minimum and median single-launch duration over up to 20
+  further launches after the timed region, each between its own event pair.
 * ``counters``: MFMA busy % and LDS bank-conflict % from the committed
   rocprofv3 summary, with the workload they were measured on, and
   ``driver_form``: the committed per-dispatch reconciliation of this command's
@@ -330,6 +332,28 @@ def time_region(call, steps):
     return a.elapsed_time(b) / steps, wall
 
 
+def launch_spread(call, n):
+    """Minimum and median duration (ms) of single launches: `n` further
+    launches after the timed region, each between its own pair of HIP events
+    on the current stream. Reported beside the timed region's average, never
+    in its place (the events between launches add their own few microseconds
+    to short kernels)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record(stream)
+        call()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    return {"n": n, "ms_min": round(ms[0], 4), "ms_median": round(ms[n // 2], 4),
+            "pass": "single launches, one HIP event pair each, after the timed region"}
+
+
 CONFIG_LEGS = ("c2", "c3", "c4", "c5")
 
 
@@ -411,6 +435,7 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     value = flops * args.steps / wall / 1e12
     achieved = flops / (avg_ms * 1e-3) / 1e12
+    spread = launch_spread(lambda: attn(q, k, v, scale), min(args.steps, 20))
 
     # The committed counter summary covers the north-star fp16 kernel only.
     north_star = args.workload == "ns" and args.dtype == "fp16"
@@ -453,6 +478,7 @@ def main():
             "min_hbm_bytes_per_launch": 2 * (2 * w["B"] * w["H"] * w["Sq"] * w["D"]
                                              + 2 * w["B"] * w["H"] * w["Skv"] * w["D"]),
         },
+        "launches": spread,
         "counters": {"mfma_busy_pct": prof["mfma_busy_pct"],
                      "lds_bank_conflict_pct": prof["lds_bank_conflict_pct"],
                      "workload": prof["counters_workload"],
