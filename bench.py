@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "attn fwd TFLOP/s + % fp16 MFMA peak, B1 H16 S16K D128, 1×MI355X"
 PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+PEAK_HBM_TBS = 8.0  # MI355X HBM3E
 WORKLOAD = dict(B=1, H=16, Sq=16384, Skv=16384, D=128)
 SEED = 106
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_ns_pmc.txt")
@@ -436,6 +437,8 @@ def main():
     value = flops * args.steps / wall / 1e12
     achieved = flops / (avg_ms * 1e-3) / 1e12
     spread = launch_spread(lambda: attn(q, k, v, scale), min(args.steps, 20))
+    min_bytes = 2 * (2 * w["B"] * w["H"] * w["Sq"] * w["D"]
+                     + 2 * w["B"] * w["H"] * w["Skv"] * w["D"])
 
     # The committed counter summary covers the north-star fp16 kernel only.
     north_star = args.workload == "ns" and args.dtype == "fp16"
@@ -475,8 +478,11 @@ def main():
             "traffic": prof["traffic"],
             "kernel_ms_avg": round(avg_ms, 4),
             "algorithmic_flops_per_launch": flops,
-            "min_hbm_bytes_per_launch": 2 * (2 * w["B"] * w["H"] * w["Sq"] * w["D"]
-                                             + 2 * w["B"] * w["H"] * w["Skv"] * w["D"]),
+            "min_hbm_bytes_per_launch": min_bytes,
+            # the same minimum bytes over the launch time against 8 TB/s, and
+            # the softmax's exponentials per launch (one per query-key pair)
+            "min_hbm_frac": round(min_bytes / (avg_ms * 1e-3) / (PEAK_HBM_TBS * 1e12), 4),
+            "exp_per_launch": w["B"] * w["H"] * w["Sq"] * w["Skv"],
         },
         "launches": spread,
         "counters": {"mfma_busy_pct": prof["mfma_busy_pct"],
