@@ -17,7 +17,9 @@ resident in HBM. Prints one JSON line with the driver's fields plus:
   ``driver_form``: the committed per-dispatch reconciliation of this command's
   short form (SQ clock x useful MFMA cycles against the measured frac).
 * ``cpu_baseline``: torch SDPA MATH on the host CPU (the oracle's routine)
-  over the whole workload, chunked by head and 2048 query rows.
+  over the whole workload, chunked by head and 2048 query rows (with
+  ``--workload c1`` .. ``c5`` that config's, c5 on its first 256 query rows of
+  every head against all keys).
 * ``configs``: kernel rates of BASELINE.json's configs c2-c5, each timed the
   same way after the north star's timed region (not part of it).
 
@@ -254,17 +256,20 @@ def conv3d_bench(args):
         "cpu_baseline": None if args.no_cpu else conv3d_cpu_baseline(x, w, b)}), flush=True)
 
 
-def cpu_baseline():
+def cpu_baseline(w=WORKLOAD, mults=(1.0, 1.0), seed=SEED, rows=None):
     """torch SDPA MATH on the host CPU (fp32 upcast of the same fp16 inputs,
     the oracle's routine) over the whole workload: every head and query row,
     chunked per head and by 2048 query rows (chunk times summed); one warm-up
-    chunk, then the best of 2 full passes."""
+    chunk, then the best of 2 full passes. `rows`: only the first `rows` query
+    rows of every head, against the full key range (c5's seeded 256-row slice,
+    BASELINE.json)."""
     import torch
 
     from oracle.attention import chunked_sdpa_math, make_inputs
 
-    w = WORKLOAD
-    q, k, v = make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"], seed=SEED)
+    q, k, v = make_inputs(w["B"], w["H"], w["Sq"], w["Skv"], w["D"], *mults, seed=seed)
+    if rows is not None:
+        q = q[:, :, :rows]
     scale = w["D"] ** -0.5
     chunked_sdpa_math(q[:, :1, :2048], k[:, :1], v[:, :1], scale)  # warm-up
     best = float("inf")
@@ -272,16 +277,18 @@ def cpu_baseline():
         t0 = time.perf_counter()
         chunked_sdpa_math(q, k, v, scale)
         best = min(best, time.perf_counter() - t0)
-    flops = 4 * w["B"] * w["H"] * w["Sq"] * w["Skv"] * w["D"]
+    flops = 4 * q.shape[0] * q.shape[1] * q.shape[2] * w["Skv"] * w["D"]
+    what = ("the whole workload" if rows is None else
+            f"the first {rows} query rows of every head against all {w['Skv']} keys")
     return {
         "value": round(flops / best / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"torch SDPA MATH (fp32 upcast) on CPU over the whole workload: all "
-                   f"{w['H']} heads, Sq=Skv={w['Sq']}, D={w['D']}, chunked by 2048 query rows "
-                   f"(times summed), best of 2 passes after a warm-up chunk: {best:.2f} s; "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "sample": (f"torch SDPA MATH (fp32 upcast) on CPU over {what}: B={w['B']}, "
+                   f"{w['H']} heads, Sq={w['Sq']}, Skv={w['Skv']}, D={w['D']}, chunked by "
+                   f"2048 query rows (times summed), best of 2 passes after a warm-up chunk: "
+                   f"{best:.3f} s; os.cpu_count()={os.cpu_count()}"),
     }
 
 
@@ -499,6 +506,9 @@ def main():
         result["configs"] = other_configs(attn, args.steps)
     if not args.no_cpu and args.workload == "ns" and args.dtype == "fp16":
         result["cpu_baseline"] = cpu_baseline()
+    elif not args.no_cpu and args.workload in CONFIGS and args.dtype == "fp16":
+        result["cpu_baseline"] = cpu_baseline(w, mults, seed,
+                                              rows=256 if args.workload == "c5" else None)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
