@@ -741,19 +741,21 @@ attn_fwd_pipe(const KArgs a) {
                 for (int nb = 0; nb < 2; ++nb) oacc[ob][nb] = E::mma16(vf, P[nb], oacc[ob][nb]);
             }
 
-            // Three V fragments ahead of the MFMAs that use them, then one
+            // kVAhead V fragments ahead of the MFMAs that use them, then one
             // more per MFMA pair (measured: +4 % north star against the
-            // compiler's own order). Every PV step is followed by a QK^T step,
-            // whose first K reads are placed ahead of this step's last
-            // kPvTail MFMAs (D = 128: +1.2 % north star and c2 with 4 or 6,
-            // -5 % with 8, which also holds back QK^T MFMAs).
-            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 6, 0);
+            // compiler's own order; D = 128 four ahead, +0.2-0.35 % north star
+            // and c2 over three, two ahead -0.7 %). Every PV step is followed
+            // by a QK^T step, whose first K reads are placed ahead of this
+            // step's last kPvTail MFMAs (D = 128: +1.2 % north star and c2
+            // with 4 or 6, -5 % with 8, which also holds back QK^T MFMAs).
+            constexpr int kVAhead = DP == 128 ? 4 : 3;  // V fragments, two reads each
+            __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * kVAhead, 0);
 #pragma unroll
-            for (int n = 0; n < NOB - 3; ++n) {
+            for (int n = 0; n < NOB - kVAhead; ++n) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(kSgMfma, 6 - kPvTail, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2 * kVAhead - kPvTail, 0);
         };
         // Scores of keys >= Skv (block keys key0..key0+31) to -inf, for the
         // last one or two blocks only.
