@@ -2140,6 +2140,11 @@ attn_fwd_d512w(const KArgs a) {
 // running max of its splits and w_s = exp2(m_s - m*),
 //     o = sum_s w_s O_s / sum_s w_s l_s
 // rounded to the element type. One thread per row and 4 consecutive dims.
+// The loads of up to kCombBatch splits go out together before any of them is
+// used: a problem small enough to be split leaves few waves per CU, so a loop
+// that waited for each split's data in turn would pay one memory latency per
+// split. The sums still run over s in ascending order.
+constexpr int kCombBatch = 4;
 struct CombArgs {
     const float* ws_o;
     const float* ws_ml;
@@ -2158,15 +2163,37 @@ __global__ void __launch_bounds__(256) attn_combine(const CombArgs c) {
     if (idx >= rows * dq) return;
     const long long row = idx / dq;
     const int d0 = (int)(idx - row * dq) * 4;
+    const int ns = c.nsplit;
+    const f32x2* ml = reinterpret_cast<const f32x2*>(c.ws_ml);
     float mx = -3.0e38f;
-    for (int s = 0; s < c.nsplit; ++s) mx = fmaxf(mx, c.ws_ml[2 * (s * rows + row)]);
+    for (int s0 = 0; s0 < ns; s0 += 2 * kCombBatch) {
+        float m[2 * kCombBatch];
+#pragma unroll
+        for (int u = 0; u < 2 * kCombBatch; ++u)
+            if (s0 + u < ns) m[u] = ml[(s0 + u) * rows + row][0];
+#pragma unroll
+        for (int u = 0; u < 2 * kCombBatch; ++u)
+            if (s0 + u < ns) mx = fmaxf(mx, m[u]);
+    }
     f32x4 acc = {};
     float l = 0.f;
-    for (int s = 0; s < c.nsplit; ++s) {
-        const long long r = s * rows + row;
-        const float w = __builtin_amdgcn_exp2f(c.ws_ml[2 * r] - mx);
-        acc += w * *reinterpret_cast<const f32x4*>(c.ws_o + r * c.D + d0);
-        l += w * c.ws_ml[2 * r + 1];
+    for (int s0 = 0; s0 < ns; s0 += kCombBatch) {
+        f32x2 mlv[kCombBatch];
+        f32x4 ov[kCombBatch];
+#pragma unroll
+        for (int u = 0; u < kCombBatch; ++u)
+            if (s0 + u < ns) {
+                const long long r = (s0 + u) * rows + row;
+                mlv[u] = ml[r];
+                ov[u] = *reinterpret_cast<const f32x4*>(c.ws_o + r * c.D + d0);
+            }
+#pragma unroll
+        for (int u = 0; u < kCombBatch; ++u)
+            if (s0 + u < ns) {
+                const float w = __builtin_amdgcn_exp2f(mlv[u][0] - mx);
+                acc += w * ov[u];
+                l += w * mlv[u][1];
+            }
     }
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const auto h0 = E::cvt2(acc[0] * inv, acc[1] * inv);
