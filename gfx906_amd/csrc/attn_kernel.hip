@@ -2378,15 +2378,29 @@ struct SplitPlan {
 size_t split_ws_bytes(const SplitPlan& p, int B, int H, int Sq, int D);
 // ws_cap bounds the workspace of the chosen plan (the static scratch's size
 // for callers that pass none); counts whose partial results do not fit are
-// skipped, down to no split at all.
+// skipped, down to no split at all. GFX906_AMD_ATTN_NSPLIT=n (tests) asks
+// for n key ranges instead of the estimate's choice, on any grid: as many
+// as there are key tiles at most, fewer where n does not divide them into
+// non-empty ranges of whole tiles (the same rule as below), and no split
+// when n = 1 or when the partial results would not fit ws_cap.
 SplitPlan plan_split(int B, int H, int Sq, int Skv, int D, size_t ws_cap = (size_t)-1) {
     const int bm = D == 512 ? Cfg512::BM : (D == 128 ? Cfg128::BM : Cfg64::BM);
     const int bn = D == 512 ? Cfg512::BN : Cfg128::BN;
     const int per_cu = D == 512 || D == 128 ? 1 : 2;
     const long long units = (long long)B * H * ((Sq + bm - 1) / bm);
-    const long long slots = (long long)cu_count() * per_cu;
-    if (Skv == 0 || units == 0 || units >= slots) return {1, 0};
+    if (Skv == 0 || units == 0) return {1, 0};
     const int tiles = (Skv + bn - 1) / bn;
+    if (const char* env = getenv("GFX906_AMD_ATTN_NSPLIT")) {
+        const long long n = atoll(env);
+        if (n >= 1) {
+            const int per = (int)((tiles + std::min<long long>(n, tiles) - 1) /
+                                  std::min<long long>(n, tiles));
+            const SplitPlan p{(tiles + per - 1) / per, per * bn};
+            return p.nsplit > 1 && split_ws_bytes(p, B, H, Sq, D) <= ws_cap ? p : SplitPlan{1, 0};
+        }
+    }
+    const long long slots = (long long)cu_count() * per_cu;
+    if (units >= slots) return {1, 0};
     const double partial_bytes = 2.0 * B * H * (double)Sq * D * 4;  // per split
     const long long cus = cu_count();
     const int step = D == 512 ? 2 : 4;

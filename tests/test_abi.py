@@ -269,6 +269,28 @@ def test_split_workspace_bytes():
         assert lib.attn_split_workspace_bytes(*bad) == 0
 
 
+@pytest.mark.parametrize("n,D,H,Skv,want", [
+    (5, 128, 1, 4096, 5),      # 64 tiles: 13 per range, the last 12
+    (7, 128, 1, 4096, 7),      # 10 per range, the last 4
+    (12, 128, 1, 4096, 11),    # 6 per range (5 would make 13 ranges): 11 ranges, the last 4
+    (13, 128, 1, 4096, 13),    # 5 per range, the last 4
+    (64, 128, 1, 4096, 64),    # one tile per range
+    (99, 128, 1, 4096, 64),    # at most one range per tile
+    (3, 512, 1, 1000, 3),      # 32 tiles of 32 keys: 11, 11, 10
+    (1, 512, 1, 4096, 1),      # no split
+    (2, 128, 16, 16384, 2),    # also a grid that fills the GPU
+])
+def test_split_count_forced_by_environment(monkeypatch, n, D, H, Skv, want):
+    """GFX906_AMD_ATTN_NSPLIT (tests) replaces the estimate's count: ranges of
+    ceil(tiles / n) whole tiles, as many as that takes."""
+    lib = gfx906_amd.capi()
+    monkeypatch.setenv("GFX906_AMD_ATTN_NSPLIT", str(n))
+    got = lib.attn_split_workspace_bytes(1, H, 1024, Skv, D)
+    assert got == (0 if want == 1 else want * H * 1024 * (D + 2) * 4 + 16)
+    monkeypatch.delenv("GFX906_AMD_ATTN_NSPLIT")
+    assert lib.attn_split_workspace_bytes(1, 16, 16384, 16384, 128) == 0
+
+
 def test_split_static_scratch_capacity_and_validation():
     lib = gfx906_amd.capi()
     cap = lib.attn_split_scratch_capacity()

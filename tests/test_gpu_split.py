@@ -64,6 +64,35 @@ def test_split_matches_unsplit_and_sdpa(dtype, B, H, Sq, Skv, D):
         assert ok, (mx, mn)
 
 
+@pytest.mark.parametrize("D,Sq,Skv", [(64, 700, 2200), (128, 300, 2500), (512, 200, 1500)])
+def test_every_split_count_matches_unsplit_and_sdpa(monkeypatch, D, Sq, Skv):
+    # Split counts forced from 2 to 17 and one range per key tile: the
+    # merge's batches of four splits and its ragged last batch, and the split
+    # kernels on ranges of a single (last: partial) tile.
+    B, H = 1, 2
+    q, k, v = (t.to(DEV) for t in make_inputs(B, H, Sq, Skv, D, 1.0, 1.0, seed=D + Sq))
+    ref = torch.empty_like(q)
+    call("ex", q, k, v, ref, D ** -0.5, F16)
+    exact = sdpa_math_fp32(q.float().cpu(), k.float().cpu(), v.float().cpu(), D ** -0.5)
+    tiles = -(-Skv // (32 if D == 512 else 64))
+    counts = set()
+    for n in list(range(2, 18)) + [tiles]:
+        monkeypatch.setenv("GFX906_AMD_ATTN_NSPLIT", str(n))
+        nbytes, ws = workspace(B, H, Sq, Skv, D)
+        per = -(-tiles // n)
+        ns = -(-tiles // per)
+        assert nbytes == ns * B * H * Sq * (D + 2) * 4 + 16
+        counts.add(ns)
+        o = torch.full_like(q, float("nan"))
+        call("split", q, k, v, o, D ** -0.5, F16, ws=ws)
+        d = (o.float() - ref.float()).abs().max().item()
+        ok, mx, mn = within_tolerance(o.float().cpu(), exact)
+        print(f"D{D} n={n} -> {ns} splits: vs unsplit {d:.2e}, vs SDPA {mx:.2e} / {mn:.2e}",
+              flush=True)
+        assert d <= 2e-3 and ok, (n, d, mx, mn)
+    assert len(counts) >= 9 and tiles in counts
+
+
 def test_split_token_contiguous_d512_and_workspace_reuse():
     # VAE views through the in-place kernel, split; then a second, smaller
     # problem on the same workspace.
