@@ -2607,7 +2607,14 @@ int scratch_setup(int dev) {
     hipEvent_t ev = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e == hipSuccess && !p) e = hipErrorInvalidSymbol;
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    // The event only orders kernels of this device on two of its streams
+    // (hipStreamWaitEvent); nothing on the host or on another device inspects
+    // it, so its record needs no system-scope fence: the kernels' own release
+    // at their end makes the scratch visible to the device's later kernels.
+    // Without the fence a call that splits costs about 2 us less of GPU time
+    // (measured on MI355X: B1 H1 S1024 D64 through launch() 16.3 -> 14.5 us).
+    if (e == hipSuccess)
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming | hipEventDisableSystemFence);
     if (dev != cur) {
         const hipError_t r = hipSetDevice(cur);
         if (e == hipSuccess) e = r;
