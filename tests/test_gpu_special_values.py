@@ -5,8 +5,9 @@ parity target) propagates a NaN in a query row to that output row only, a
 NaN in any key row to every output row of its head (the key's score enters
 every row's softmax), and a NaN in any value row to every output row of its
 head (0 * NaN is NaN even where the weight underflows). The kernel's running
-maximum, its rescale tests and its split-key merge must keep exactly that
-pattern and leave every other row at the usual bar. Each case prints its
+maximum, its rescale tests and its split-key merge (each case runs with the
+op's own plan and with its keys forced into three ranges) must keep exactly
+that pattern and leave every other row at the usual bar. Each case prints its
 parameters first.
 """
 
@@ -30,10 +31,15 @@ CASES = [  # B, H, Sq, Skv, D
 ]
 
 
+@pytest.mark.parametrize("nsplit", [None, 3])
 @pytest.mark.parametrize("B,H,Sq,Skv,D", CASES)
 @pytest.mark.parametrize("where", ["q", "k", "v"])
-def test_nan_pattern_matches_sdpa(B, H, Sq, Skv, D, where):
-    print(f"case nan in {where}: B{B} H{H} Sq{Sq} Skv{Skv} D{D}", flush=True)
+def test_nan_pattern_matches_sdpa(monkeypatch, B, H, Sq, Skv, D, where, nsplit):
+    # nsplit: the op's own plan, or the key range forced into three ranges
+    # (GFX906_AMD_ATTN_NSPLIT), so that the NaN passes through the merge.
+    if nsplit:
+        monkeypatch.setenv("GFX906_AMD_ATTN_NSPLIT", str(nsplit))
+    print(f"case nan in {where}: B{B} H{H} Sq{Sq} Skv{Skv} D{D} nsplit {nsplit}", flush=True)
     q, k, v = make_inputs(B, H, Sq, Skv, D, 1.0, 1.0, 7)
     t = {"q": q, "k": k, "v": v}[where]
     rows = t.shape[2]
