@@ -248,6 +248,31 @@ def test_sharp_softmax_c3_like():
     check_full(1, 2, 256, 512, 64, qk_mult=2.0, seed=12)
 
 
+@pytest.mark.parametrize("nsplit", [2, 5])
+@pytest.mark.parametrize("D", [40, 64, 128, 512])
+def test_semantics_with_forced_splits(monkeypatch, D, nsplit):
+    # The edge cases above again with the key range split (the attn_fwd entry
+    # point, static scratch; GFX906_AMD_ATTN_NSPLIT forces the count): a
+    # negative and a zero scale, sharp rows, a single key, and a score step
+    # that the running max of one split never sees.
+    monkeypatch.setenv("GFX906_AMD_ATTN_NSPLIT", str(nsplit))
+    check_full(1, 2, 100, 700, D, scale=-(D ** -0.5), seed=40 + D)
+    q, k, v = make_inputs(1, 2, 64, 700, D, seed=41 + D)
+    out = run_capi(q.to(DEV), k.to(DEV), v.to(DEV), 0.0).cpu().float()
+    assert_close(out, v.double().mean(dim=2, keepdim=True).expand_as(out), f"scale 0 D{D}")
+    check_full(1, 2, 256, 700, D, qk_mult=2.0, seed=42 + D)
+    q, k, v = make_inputs(1, 2, 33, 1, D, seed=43 + D)
+    out = run_capi(q.to(DEV), k.to(DEV), v.to(DEV), 0.1).cpu()
+    assert torch.equal(out, v.expand_as(out))
+    q, k, v = make_inputs(1, 2, 96, 700, D, seed=44 + D)
+    q = torch.ones_like(q) * 0.25
+    k = torch.zeros_like(k)
+    scale = D ** -0.5
+    k[:, :, 400:, :] = 17.0 / (D * 0.25 * scale * 1.4426950408889634)
+    out = run_capi(q.to(DEV), k.to(DEV), v.to(DEV), scale)
+    assert_close(out, sdpa_math_fp32(q, k, v, scale), f"score step, {nsplit} splits, D{D}")
+
+
 def test_large_scores_rescale():
     # Scores growing along the key axis force repeated running-max updates.
     q, k, v = make_inputs(1, 1, 64, 1024, 128, seed=13)
