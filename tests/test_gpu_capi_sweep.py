@@ -11,6 +11,9 @@ does (ctypes, element strides per tensor) and runs every case three ways:
 * ``attn_fwd_split_static``: the same split in the library's static scratch,
   which must give the same bits as the caller-workspace call.
 
+In about half the cases the two split calls run with a forced split count (2 to 9,
+GFX906_AMD_ATTN_NSPLIT), also on grids the planner would not split.
+
 Each case draws a head dim from every class, fp16 or bf16, B and H, ragged Sq
 and Skv (up to 2500 keys, so Q through LDS and several splits occur), a scale
 of either sign, and a layout per tensor (contiguous, [B, S, H, D] transpose,
@@ -93,8 +96,15 @@ def lib():
 
 
 @pytest.mark.parametrize("i", range(N_CASES))
-def test_capi_random_case(lib, i):
+def test_capi_random_case(lib, i, monkeypatch):
     c, rng = draw_case(i)
+    # About half the cases force the split count (GFX906_AMD_ATTN_NSPLIT, 2..9) for
+    # the two split calls, from a generator of its own so that the cases'
+    # other draws stay as they were.
+    ns = int(np.random.default_rng(1_000_000 + i).integers(0, 18))
+    c["nsplit"] = ns if ns >= 2 and ns <= 9 else None
+    if c["nsplit"]:
+        monkeypatch.setenv("GFX906_AMD_ATTN_NSPLIT", str(c["nsplit"]))
     print(c, flush=True)
     B, H, Sq, Skv, D = c["B"], c["H"], c["Sq"], c["Skv"], c["D"]
     q, k, v = make_inputs(B, H, Sq, Skv, D, c["qk_mult"], 1.0, c["seed"])
