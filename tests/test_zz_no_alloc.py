@@ -8,8 +8,8 @@ device scratch) through the C ABI:
 * a problem whose caller-workspace plan does not fit the scratch runs with
   the best plan that does (here none) and equals attn_fwd_ex bit for bit;
 * captured in a CUDA graph and replayed, with eager calls between replays;
-* issued on two streams at once, overlapping: the calls that use the scratch
-  are ordered on the GPU, so every result equals its serial one;
+* issued on three streams at once, overlapping: the calls that use the
+  scratch are ordered on the GPU, so every result equals its serial one;
 * launch() and attn_fwd(), which split small grids through the same scratch.
 """
 
@@ -152,7 +152,8 @@ def test_static_scratch_under_graph_capture():
 
 def test_static_scratch_ordered_across_streams():
     lib = gfx906_amd.capi()
-    cases = [(1, 1, 4096, 16384, 512), (1, 1, 2048, 4096, 512), (1, 2, 1024, 6000, 128)]
+    cases = [(1, 1, 4096, 16384, 512), (1, 1, 2048, 4096, 512), (1, 2, 1024, 6000, 128),
+             (1, 1, 1024, 1024, 64)]
     data, refs = [], []
     for n, (B, H, Sq, Skv, D) in enumerate(cases):
         (_, _, _), (q, k, v) = _inputs(B, H, Sq, Skv, D, 300 + n)
@@ -161,15 +162,15 @@ def test_static_scratch_ordered_across_streams():
         data.append((q, k, v, D ** -0.5))
         refs.append(ref)
     torch.cuda.synchronize()
-    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()]
     main = torch.cuda.current_stream()
-    for it in range(4):
-        print(f"case: two streams, iteration {it}", flush=True)
-        outs = [[torch.full_like(d[0], float("nan")) for d in data] for _ in range(2)]
+    for it in range(8):
+        print(f"case: three streams, iteration {it}", flush=True)
+        outs = [[torch.full_like(d[0], float("nan")) for d in data] for _ in streams]
         for s in streams:
             s.wait_stream(main)
-        # Each case runs on both streams, the two streams interleaved call by
-        # call: the static entry point on one, launch() on the other.
+        # Each case runs on every stream, the streams interleaved call by call:
+        # the static entry point on some, launch() on the others.
         for n, (q, k, v, scale) in enumerate(data):
             for j, s in enumerate(streams):
                 with torch.cuda.stream(s):
@@ -178,7 +179,7 @@ def test_static_scratch_ordered_across_streams():
                     else:
                         _launch(lib, q, k, v, scale, outs[j][n])
         torch.cuda.synchronize()
-        for j in range(2):
+        for j in range(len(streams)):
             for n in range(len(data)):
                 assert torch.equal(outs[j][n], refs[n]), (it, j, n)
 
