@@ -21,11 +21,12 @@ padded sequence stride, K/V shared by every head with head stride 0, and for
 D = 512 the token-contiguous K/V of a [b, c, h*w] activation). Outputs of the
 first two calls are held to the bars of the other parity tests against SDPA
 MATH in fp32 on the CPU (fp16 2e-3 / 2e-4, bf16 eight times that), except
-where the output format's spacing leaves no room under the max bar: there an
+where the output format's spacing leaves no room under the bars: there an
 element may be off by half a unit in the last place of the reference plus the
-mean bar (within_rounded_tolerance; fp16 from |o| >= 4, where the correctly
-rounded output alone errs by up to 1.95e-3). Each case prints its parameters
-first.
+mean bar (fp16 from |o| >= 4, where the correctly rounded output alone errs by
+up to 1.95e-3), and the mean error may reach that of the correctly rounded
+reference plus half the mean bar (within_rounded_tolerance). Each case prints
+its parameters first.
 """
 
 import ctypes

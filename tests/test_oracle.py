@@ -166,7 +166,7 @@ def test_rounded_tolerance_takes_the_output_format_spacing():
     the bar is the plain 2e-3; from 4 to 8 it is half an ulp (1.95e-3) plus the
     mean bar, which passes the seeded sweep's element whose exact value,
     4.037011, lies 1e-4 below the midpoint of 4.0352 and 4.0391, and one ulp
-    further fails. The mean bar is unchanged."""
+    further fails. Outputs exact in fp16 keep the plain mean bar."""
     rng = np.random.default_rng(3)
     # a few large values among many exact small ones (a mean like an output's)
     ref = np.concatenate([rng.uniform(-12, 12, 96), rng.integers(-256, 256, 4000) / 256])
@@ -184,7 +184,8 @@ def test_rounded_tolerance_takes_the_output_format_spacing():
 
 def test_rounded_tolerance_bf16_form():
     """bf16 at eight times the bars: half a bf16 ulp (8 significant bits) plus
-    1.6e-3, at least 1.6e-2, element by element; the mean bar 1.6e-3."""
+    1.6e-3, at least 1.6e-2, element by element; the mean bar 1.6e-3 for
+    references exact in bf16."""
     for ref, half_ulp in ((0.5, 2 ** -9), (3.0, 2 ** -7), (7.5, 2 ** -6), (12.0, 2 ** -5),
                           (100.0, 2 ** -2)):
         allowed = max(half_ulp + 8 * 2e-4, 8 * 2e-3)
@@ -192,6 +193,46 @@ def test_rounded_tolerance_bf16_form():
         assert not one(ref + 1.01 * allowed, ref, "bf16", 8), ref
     assert not oa.within_rounded_tolerance(np.full(50, 1.0 + 1.7e-3), np.ones(50), "bf16",
                                            mult=8)[0]
+
+
+def test_round_to_format_matches_torch():
+    """Round to nearest even in fp16 (subnormals included) and bf16, as torch
+    converts float32: random magnitudes from 2^-30 to 2^15, exact ties and the
+    values next to them."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(20000) * np.exp2(rng.uniform(-30, 15, 20000))).astype(np.float32)
+    ties16 = (np.arange(1, 2000, dtype=np.float64) + 0.5) * 2.0 ** -11  # fp16 midpoints in [0, 1)
+    ties_b = (np.arange(256, 512, dtype=np.float64) + 0.5) * 2.0 ** -8  # bf16 midpoints in [1, 2)
+    x = np.concatenate([x, ties16, ties_b, np.nextafter(ties_b, 0), np.nextafter(ties_b, 4)])
+    x = x.astype(np.float32).astype(np.float64)
+    for fmt, dt in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        want = torch.tensor(x, dtype=torch.float32).to(dt).double().numpy()
+        assert np.array_equal(oa.round_to_format(x, fmt), want), fmt
+
+
+def test_rounded_tolerance_mean_floor():
+    """The mean bar gives way to the format's own rounding only: values at
+    the midpoints of bf16 neighbours in [1, 2) err by half an ulp (3.9e-3)
+    each when correctly rounded, over the plain 1.6e-3 mean bar, and pass;
+    one ulp further out fails although every element stays inside its
+    element bar; an fp16 output with |o| near 1 whose errors exceed its
+    rounding by 1.3e-4 on every element fails as under the plain bar."""
+    ref = (np.arange(256, 512, dtype=np.float64) + 0.5) * 2.0 ** -8
+    rounded = oa.round_to_format(ref, "bf16")
+    assert np.abs(rounded - ref).mean() == 2.0 ** -9
+    assert not oa.within_tolerance(rounded, ref, 8 * oa.MAX_ABS_TOL, 8 * oa.MEAN_ABS_TOL)[0]
+    assert oa.within_rounded_tolerance(rounded, ref, "bf16", mult=8)[0]
+    away = rounded + np.sign(rounded - ref) * 2.0 ** -7  # the next bf16 value outward
+    ok, mx, mn = oa.within_rounded_tolerance(away, ref, "bf16", mult=8)
+    assert not ok and mx < 8 * oa.MAX_ABS_TOL
+    rng = np.random.default_rng(11)
+    r = rng.uniform(0.5, 1.0, 4000).astype(np.float32).astype(np.float64)
+    r16 = oa.round_to_format(r, "fp16")
+    assert oa.within_rounded_tolerance(r16, r, "fp16")[0]
+    worse = r16 + np.where(r16 >= r, 1.3e-4, -1.3e-4)
+    assert not oa.within_rounded_tolerance(worse, r, "fp16")[0]
 
 
 # -- kernel_numerics_model -------------------------------------------------------
